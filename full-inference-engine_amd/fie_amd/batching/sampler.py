@@ -1,0 +1,173 @@
+"""Batched per-row sampling on MI355X: the reference's call surface over HIP kernels.
+
+``BatchedSampler`` keeps the constructor, ``sample``/``forget`` and ``SampleResult``
+of the reference (engine/batching/sampler.py:32-117), so the engine's ``_sample``
+adapter (engine/batching/continuous_batching.py:1911-1931) can call it unchanged.
+What changes is underneath: one packed parameter upload, a fixed chain of fused HIP
+kernels, one packed download.  The draw is an inverse-CDF draw against a per-row
+uniform taken from the row's own generator (seeded rows) or the shared generator,
+so a seeded request's tokens do not depend on its batch neighbours.
+"""
+
+from __future__ import annotations
+
+from collections import OrderedDict
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from ..kernel import FLAG_GREEDY, FLAG_PENALTY, FusedSampler, HostParams
+from ..runtime.sampling import SamplingParams
+
+
+@dataclass
+class SampleResult:
+    """Chosen token per row, plus logprobs for the rows that asked for them
+    (engine/batching/sampler.py:32-39)."""
+
+    token_ids: list[int]
+    logprobs: dict[int, list[tuple[int, float]]]
+
+
+def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarray,
+                   contexts: list[list[int]] | None) -> HostParams:
+    """Per-row arrays for the kernels, derived the way sampler.py:109,182-192 does."""
+    rows = len(params)
+    greedy = np.fromiter((p.greedy for p in params), dtype=bool, count=rows)
+    pen = np.fromiter((p.has_penalties for p in params), dtype=bool, count=rows)
+    temps = np.fromiter((p.temperature for p in params), dtype=np.float64, count=rows)
+    top_k = np.fromiter((p.top_k for p in params), dtype=np.int64, count=rows)
+    top_p = np.fromiter((p.top_p for p in params), dtype=np.float64, count=rows)
+    min_p = np.fromiter((p.min_p for p in params), dtype=np.float64, count=rows)
+    lp = np.fromiter((-1 if p.logprobs is None else p.logprobs for p in params),
+                     dtype=np.int32, count=rows)
+    apply = bool(pen.any()) and contexts is not None
+    offsets = np.zeros(rows + 1, dtype=np.int64)
+    ids = np.zeros(0, dtype=np.int32)
+    if apply:
+        # Only penalised rows' contexts are read (sampler.py:136-139).
+        lengths = np.fromiter((len(c) if pen[i] else 0 for i, c in enumerate(contexts)),
+                              dtype=np.int64, count=rows)
+        np.cumsum(lengths, out=offsets[1:])
+        if offsets[-1]:
+            flat = np.fromiter((t for i, c in enumerate(contexts) if pen[i] for t in c),
+                               dtype=np.int64, count=int(offsets[-1]))
+            if flat.min() < 0 or flat.max() >= 2**31:
+                raise ValueError("penalty context token ids must be in [0, 2**31)")
+            ids = flat.astype(np.int32)
+    return HostParams(
+        scale=np.where(greedy, 1.0, temps).astype(np.float32),
+        top_k=np.where((top_k > 0) & (top_k < vocab) & ~greedy, top_k, 0).astype(np.int32),
+        top_p=np.where((top_p < 1.0) & ~greedy, top_p, 1.0).astype(np.float32),
+        min_p=np.where((min_p > 0.0) & ~greedy, min_p, 0.0).astype(np.float32),
+        flags=(greedy.astype(np.int32) * FLAG_GREEDY + pen.astype(np.int32) * FLAG_PENALTY),
+        logprobs=lp,
+        uniform=np.ascontiguousarray(uniforms, dtype=np.float64),
+        rep=np.fromiter((p.repetition_penalty for p in params), np.float32, count=rows),
+        pres=np.fromiter((p.presence_penalty for p in params), np.float32, count=rows),
+        freq=np.fromiter((p.frequency_penalty for p in params), np.float32, count=rows),
+        hist_off=offsets,
+        hist_ids=ids,
+        apply_penalties=apply,
+    )
+
+
+class BatchedSampler:
+    """Applies per-request sampling to one step's logits (sampler.py:42-78).
+
+    Holds no per-request state besides the seeded generators: penalties come from
+    the token ids the caller passes, so a preempted and rebuilt request samples
+    identically.
+    """
+
+    def __init__(self, device: torch.device | str, *, generator_seed: int | None = None,
+                 max_generators: int = 1024):
+        self.device = torch.device(device)
+        self._fused = FusedSampler(self.device)
+        # The shared stream for rows without their own seed.
+        self._generator = np.random.Generator(np.random.PCG64(generator_seed))
+        # Request id -> generator (sampler.py:58-61): two requests with one seed must
+        # not share a stream, so generators are keyed by request, not by seed.
+        self._seeded: OrderedDict[object, np.random.Generator] = OrderedDict()
+        self._max_generators = max_generators
+
+    def _row_generator(self, request_id: object, seed: int) -> np.random.Generator:
+        gen = self._seeded.get(request_id)
+        if gen is None:
+            gen = np.random.Generator(np.random.PCG64(seed))
+            self._seeded[request_id] = gen
+            while len(self._seeded) > self._max_generators:
+                self._seeded.popitem(last=False)
+        else:
+            self._seeded.move_to_end(request_id)
+        return gen
+
+    def forget(self, request_ids: list[object]) -> None:
+        """Drop generators for finished requests (sampler.py:75-78)."""
+        for request_id in request_ids:
+            self._seeded.pop(request_id, None)
+
+    def _uniforms(self, params: list[SamplingParams],
+                  request_ids: list[object] | None) -> np.ndarray:
+        rows = len(params)
+        u = np.zeros(rows, dtype=np.float64)
+        unseeded = [r for r, p in enumerate(params) if not p.greedy and p.seed is None]
+        if unseeded:
+            u[unseeded] = self._generator.random(len(unseeded))
+        for r, p in enumerate(params):
+            if p.greedy or p.seed is None:
+                continue
+            rid = request_ids[r] if request_ids is not None else r
+            u[r] = self._row_generator(rid, p.seed).random()
+        return u
+
+    # ------------------------------------------------------------------ the step
+    def sample(
+        self,
+        logits: torch.Tensor,
+        params: list[SamplingParams],
+        context_tokens: list[list[int]] | None = None,
+        request_ids: list[object] | None = None,
+    ) -> SampleResult:
+        """Choose one token per row (sampler.py:81-117)."""
+        if logits.ndim != 2:
+            raise ValueError("logits must have shape [rows, vocab]")
+        rows, vocab = logits.shape
+        if len(params) != rows:
+            raise ValueError("one SamplingParams per logits row is required")
+        if context_tokens is not None and len(context_tokens) != rows:
+            raise ValueError("one context per logits row is required")
+        if request_ids is not None and len(request_ids) != rows:
+            raise ValueError("one request id per logits row is required")
+        if rows == 0:
+            return SampleResult([], {})
+
+        wants_logprobs = any(p.logprobs is not None for p in params)
+        plain = all(p.greedy and not p.has_penalties for p in params)
+        if plain and not wants_logprobs:
+            # sampler.py:103-106: one argmax kernel and one device-to-host copy.
+            return SampleResult(self._fused.argmax(logits).tolist(), {})
+
+        hp = resolve_params(params, vocab, self._uniforms(params, request_ids), context_tokens)
+        out, _, _ = self._fused.step(logits, hp)
+        tokens = [int(t) for t in out["tokens"]]
+        return SampleResult(tokens, self._logprobs(params, tokens, out))
+
+    @staticmethod
+    def _logprobs(params: list[SamplingParams], chosen: list[int],
+                  out: dict[str, np.ndarray]) -> dict[int, list[tuple[int, float]]]:
+        """Chosen-token logprob first, then the row's best alternatives
+        (sampler.py:262-291)."""
+        result: dict[int, list[tuple[int, float]]] = {}
+        for row, p in enumerate(params):
+            if p.logprobs is None:
+                continue
+            count = p.logprobs
+            entries = [(chosen[row], float(out["chosen_lp"][row]))]
+            ids = out["top_ids"][row][:count]
+            vals = out["top_lp"][row][:count]
+            entries.extend((int(t), float(v)) for t, v in zip(ids, vals)
+                           if t >= 0 and int(t) != chosen[row])
+            result[row] = entries[:count + 1]
+        return result

@@ -1,0 +1,357 @@
+/*
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product may load or call this file.
+ *
+ * Plain-C restatement of the reference token sampler
+ *   engine/batching/sampler.py:81-291  (BatchedSampler.sample and its stages)
+ *   engine/runtime/sampling.py:71-79   (greedy / has_penalties predicates)
+ * written as the checker for the HIP sampler.  Every stage follows the reference
+ * line it cites; the places where the reference leaves the result to ATen's float
+ * rounding (top-p boundary bits, tie order under an unstable sort, the multinomial
+ * stream) are replaced by the build's canonical rules, stated where they are used:
+ *
+ *   (R1) weights     W_i = floor(cexp(y_i - M) * 2^40), an integer; all mass sums
+ *                    are exact 64-bit integer sums, so no summation order matters.
+ *   (R2) order       tokens are ranked by (y descending, token index ascending).
+ *   (R3) top-p       token at rank j is dropped iff  sum_{rank<j} W >= p * S,
+ *                    evaluated exactly (p is the fp32 value of top_p).
+ *   (R4) draw        t = floor(u * T) with T the kept mass; the token is the first
+ *                    kept token in (R2) order whose inclusive prefix mass exceeds t.
+ *   (R5) min-p       token dropped iff cexp(y_i - M) < fp32(min_p).
+ *   (R6) top_p == 1  drops nothing (the exact-arithmetic reading of the reference's
+ *                    `cumulative - p >= 1.0` test, sampler.py:226).
+ *   (R7) logprobs    lse = M + ln(S_all / 2^40), S_all the weight sum over the row.
+ *
+ * cexp() is the build's own fp32 exponential: Cody-Waite reduction by ln 2 (split
+ * constant), a degree-7 Taylor polynomial for e^r on |r| <= ln2/2 evaluated by
+ * Horner with fused multiply-adds, and an exact scaling by 2^n.  Every operation is
+ * an IEEE-754 binary32 operation with round-to-nearest-even, so the HIP kernels,
+ * which perform the same operations in the same order, produce the same bits.
+ * Compile with -ffp-contract=off so the compiler adds no fusions of its own.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------ arithmetic */
+
+float oracle_cexp(float d)
+{
+    if (!(d > -80.0f)) return 0.0f;          /* -inf, NaN and deep underflow */
+    if (d >= 0.0f) return 1.0f;              /* y - M is never positive */
+    float n = rintf(d * 1.44269502f);        /* round(d / ln 2) */
+    float r = fmaf(n, -0.693145752f, d);     /* ln2 high part, 16 significant bits */
+    r = fmaf(n, -1.42860677e-06f, r);        /* ln2 low part */
+    float p = 1.98412701e-04f;               /* 1/7! */
+    p = fmaf(p, r, 1.38888892e-03f);         /* 1/6! */
+    p = fmaf(p, r, 8.33333377e-03f);         /* 1/5! */
+    p = fmaf(p, r, 4.16666679e-02f);         /* 1/4! */
+    p = fmaf(p, r, 1.66666672e-01f);         /* 1/3! */
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    return ldexpf(p, (int)n);
+}
+
+static inline uint64_t weight_of(float e)
+{
+    return (uint64_t)((double)e * 1099511627776.0);   /* floor(e * 2^40), exact */
+}
+
+/* Order-preserving key of an fp32 value: larger value, larger key. */
+static inline uint32_t fkey(float y)
+{
+    uint32_t b;
+    memcpy(&b, &y, 4);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+/* (R2): descending composite = descending value, then ascending index. */
+static inline uint64_t comp_of(float y, int32_t idx)
+{
+    return ((uint64_t)fkey(y) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+static inline int32_t idx_of(uint64_t comp)
+{
+    return (int32_t)(0xFFFFFFFFu - (uint32_t)(comp & 0xFFFFFFFFu));
+}
+
+static int cmp_desc_u64(const void* a, const void* b)
+{
+    uint64_t x = *(const uint64_t*)a, y = *(const uint64_t*)b;
+    return (x < y) - (x > y);
+}
+
+/* ceil(p * S) for fp32 p in (0,1) and integer S < 2^63, exactly. */
+static uint64_t ceil_mul_f32(float p, uint64_t S)
+{
+    int e;
+    float m = frexpf(p, &e);                     /* p = m * 2^e, m in [0.5,1) */
+    uint64_t mi = (uint64_t)ldexpf(m, 24);       /* 24-bit integer mantissa */
+    int q = 24 - e;                              /* p = mi / 2^q, q >= 24 */
+    unsigned __int128 prod = (unsigned __int128)mi * S;
+    if (q >= 127) return prod ? 1 : 0;
+    unsigned __int128 fl = prod >> q;
+    unsigned __int128 rem = prod - (fl << q);
+    return (uint64_t)(fl + (rem ? 1 : 0));
+}
+
+/* floor(u * T) for double u in [0,1) and integer T < 2^63, exactly. */
+static uint64_t floor_mul_f64(double u, uint64_t T)
+{
+    if (!(u > 0.0)) return 0;
+    int e;
+    double m = frexp(u, &e);                     /* u = m * 2^e */
+    uint64_t mi = (uint64_t)ldexp(m, 53);
+    int q = 53 - e;                              /* u = mi / 2^q, q >= 53 */
+    unsigned __int128 prod = (unsigned __int128)mi * T;
+    if (q >= 127) return 0;
+    return (uint64_t)(prod >> q);
+}
+
+/* ------------------------------------------------------------------ penalties */
+
+typedef struct { int32_t id; int32_t pos; } occ_t;
+typedef struct { int32_t id; int32_t count; int32_t first; } uniq_t;
+
+static int cmp_occ(const void* a, const void* b)
+{
+    const occ_t *x = a, *y = b;
+    if (x->id != y->id) return (x->id > y->id) - (x->id < y->id);
+    return (x->pos > y->pos) - (x->pos < y->pos);
+}
+
+static int cmp_first(const void* a, const void* b)
+{
+    const uniq_t *x = a, *y = b;
+    return (x->first > y->first) - (x->first < y->first);
+}
+
+/* Distinct ids of one context in first-occurrence order with their counts, exactly
+ * the insertion order of the reference's `occurrences` dict (sampler.py:140-144). */
+static int32_t unique_in_order(const int32_t* ids, int64_t n, uniq_t* out, occ_t* tmp)
+{
+    for (int64_t i = 0; i < n; ++i) { tmp[i].id = ids[i]; tmp[i].pos = (int32_t)i; }
+    qsort(tmp, (size_t)n, sizeof(occ_t), cmp_occ);
+    int32_t u = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        if (i == 0 || tmp[i].id != tmp[i - 1].id) {
+            out[u].id = tmp[i].id; out[u].count = 1; out[u].first = tmp[i].pos; ++u;
+        } else {
+            out[u - 1].count += 1;
+        }
+    }
+    qsort(out, (size_t)u, sizeof(uniq_t), cmp_first);
+    return u;
+}
+
+/*
+ * _apply_penalties, sampler.py:120-175, in place on w[B*V].
+ * The gather reads the unpenalised logits; the scatter then writes, for every row,
+ * `width` entries in column order (real entries first, pad entries after), and a
+ * later write to the same index replaces an earlier one, as a sequential scatter
+ * does.  Pad entries and ids >= V target index 0 with the original logit of token 0
+ * (sampler.py:156-157,174), which is how a real token-0 penalty can be undone (Q1).
+ * Returns the batch width, or -1 on a negative id.
+ */
+int32_t oracle_penalize(float* w, int32_t B, int32_t V, const uint8_t* has_pen,
+                        const float* rep, const float* pres, const float* freq,
+                        const int64_t* off, const int32_t* ids)
+{
+    int64_t maxn = 0;
+    for (int32_t r = 0; r < B; ++r) {
+        int64_t n = off[r + 1] - off[r];
+        if (n > maxn) maxn = n;
+        for (int64_t i = off[r]; i < off[r + 1]; ++i) if (ids[i] < 0) return -1;
+    }
+    if (B <= 0) return 0;
+    uniq_t** rows = calloc((size_t)(uint32_t)B, sizeof(uniq_t*));
+    int32_t* nu = calloc((size_t)(uint32_t)B, sizeof(int32_t));
+    occ_t* tmp = malloc((size_t)(maxn ? maxn : 1) * sizeof(occ_t));
+    int32_t width = 0;
+    for (int32_t r = 0; r < B; ++r) {
+        int64_t n = off[r + 1] - off[r];
+        if (!has_pen[r] || n == 0) continue;
+        rows[r] = malloc((size_t)n * sizeof(uniq_t));
+        nu[r] = unique_in_order(ids + off[r], n, rows[r], tmp);
+        if (nu[r] > width) width = nu[r];
+    }
+    if (width > 0) {
+        for (int32_t r = 0; r < B; ++r) {
+            float* row = w + (int64_t)r * V;
+            float g0 = row[0];
+            /* gather every value first: the scatter source is built from the input */
+            float* src = malloc((size_t)width * sizeof(float));
+            int32_t* dst = malloc((size_t)width * sizeof(int32_t));
+            for (int32_t j = 0; j < width; ++j) {
+                if (j < nu[r] && rows[r][j].id < V) {
+                    float g = row[rows[r][j].id];
+                    float pen = (g > 0.0f) ? g / rep[r] : g * rep[r];
+                    pen = pen - pres[r];
+                    pen = pen - freq[r] * (float)rows[r][j].count;
+                    src[j] = pen;
+                    dst[j] = rows[r][j].id;
+                } else {
+                    src[j] = g0;
+                    dst[j] = 0;
+                }
+            }
+            for (int32_t j = 0; j < width; ++j) row[dst[j]] = src[j];
+            free(src); free(dst);
+        }
+    }
+    for (int32_t r = 0; r < B; ++r) free(rows[r]);
+    free(rows); free(nu); free(tmp);
+    return width;
+}
+
+/* ------------------------------------------------------------------ one step */
+
+typedef struct {
+    int32_t B, V;
+    float* logits;                 /* [B*V] fp32, modified in place by penalties */
+    const float* scale;            /* divisor: fp32(temperature), 1.0 for greedy rows */
+    const int32_t* top_k;          /* effective k, 0 = off */
+    const float* top_p;            /* effective p, 1.0 = off */
+    const float* min_p;            /* effective min_p, 0 = off */
+    const uint8_t* greedy;
+    const int32_t* logprobs;       /* -1 = none, else 0..20 */
+    const double* uniform;         /* [B], in [0,1) */
+    int32_t apply_penalties;
+    const uint8_t* has_pen;
+    const float *rep, *pres, *freq;
+    const int64_t* hist_off;       /* [B+1] */
+    const int32_t* hist_ids;
+    int32_t lp_cols;               /* columns of top_ids/top_lp */
+    /* outputs */
+    int64_t* tokens;               /* [B] */
+    uint32_t* tk_key;              /* [B] top-k threshold key (0 = none) */
+    uint64_t* cut_comp;            /* [B] composite key of the last top-p survivor (0 = none) */
+    float* row_max;                /* [B] M */
+    uint64_t* t_kept;              /* [B] kept mass */
+    uint64_t* s_all;               /* [B] whole-row mass */
+    uint8_t* kept;                 /* [B*V] or NULL */
+    float* probs;                  /* [B*V] or NULL */
+    float* chosen_lp;              /* [B] or NULL */
+    int64_t* top_ids;              /* [B*lp_cols] or NULL */
+    float* top_lp;                 /* [B*lp_cols] or NULL */
+} oracle_args;
+
+int32_t oracle_sample(oracle_args* a)
+{
+    const int32_t B = a->B, V = a->V;
+    if (a->apply_penalties) {
+        if (oracle_penalize(a->logits, B, V, a->has_pen, a->rep, a->pres, a->freq,
+                            a->hist_off, a->hist_ids) < 0) return -1;
+    }
+    float* y = malloc((size_t)V * sizeof(float));
+    float* e = malloc((size_t)V * sizeof(float));
+    uint64_t* order = malloc((size_t)V * sizeof(uint64_t));
+    uint8_t* surv = malloc((size_t)V);
+    for (int32_t r = 0; r < B; ++r) {
+        const float* w = a->logits + (int64_t)r * V;
+        const float s = a->scale[r];
+        /* _apply_temperature, sampler.py:177-185: a true fp32 divide per element */
+        uint32_t best = 0;
+        int32_t amax = 0;
+        for (int32_t i = 0; i < V; ++i) {
+            y[i] = w[i] / s + 0.0f;                  /* +0.0f folds -0 into +0 */
+            if (i == 0 || fkey(y[i]) > best) { best = fkey(y[i]); amax = i; }
+        }
+        const float M = y[amax];
+        a->row_max[r] = M;
+        uint64_t sall = 0;
+        for (int32_t i = 0; i < V; ++i) {
+            e[i] = oracle_cexp(y[i] - M);
+            sall += weight_of(e[i]);
+        }
+        a->s_all[r] = sall;
+        a->tk_key[r] = 0;
+        a->cut_comp[r] = 0;
+        int need_sort = a->greedy[r] ? (a->logprobs[r] > 0) : 1;
+        if (need_sort) {
+            for (int32_t i = 0; i < V; ++i) order[i] = comp_of(y[i], i);
+            qsort(order, (size_t)V, sizeof(uint64_t), cmp_desc_u64);
+        }
+        if (a->greedy[r]) {
+            /* _draw greedy rows, sampler.py:236-238: argmax, first index on ties */
+            a->tokens[r] = amax;
+            a->t_kept[r] = weight_of(1.0f);
+            if (a->kept) memset(a->kept + (int64_t)r * V, 1, (size_t)V);
+            if (a->probs) {
+                memset(a->probs + (int64_t)r * V, 0, (size_t)V * sizeof(float));
+                a->probs[(int64_t)r * V + amax] = 1.0f;
+            }
+        } else {
+            /* _filter top-k, sampler.py:194-209: keep y >= k-th largest value */
+            uint32_t tk = 0;
+            if (a->top_k[r] > 0) {
+                tk = (uint32_t)(order[a->top_k[r] - 1] >> 32);
+                a->tk_key[r] = tk;
+            }
+            /* _filter min-p, sampler.py:211-218, rule (R5) */
+            const float mp = a->min_p[r];
+            uint64_t S = 0;
+            for (int32_t i = 0; i < V; ++i) {
+                surv[i] = (fkey(y[i]) >= tk) && !(mp > 0.0f && e[i] < mp);
+                if (surv[i]) S += weight_of(e[i]);
+            }
+            /* _filter top-p, sampler.py:220-228, rules (R2)(R3)(R6) */
+            const float p = a->top_p[r];
+            uint64_t T = 0;
+            uint64_t thr = (p < 1.0f) ? ceil_mul_f32(p, S) : UINT64_MAX;
+            uint64_t excl = 0;
+            int stopped = 0;
+            for (int32_t j = 0; j < V; ++j) {
+                int32_t i = idx_of(order[j]);
+                if (!surv[i]) continue;
+                if (stopped || excl >= thr) { stopped = 1; surv[i] = 0; continue; }
+                excl += weight_of(e[i]);
+                if (p < 1.0f) a->cut_comp[r] = order[j];
+            }
+            for (int32_t i = 0; i < V; ++i) if (surv[i]) T += weight_of(e[i]);
+            a->t_kept[r] = T;
+            /* _draw sampled rows, sampler.py:241-259, replaced by rule (R4) */
+            uint64_t t = floor_mul_f64(a->uniform[r], T);
+            uint64_t incl = 0;
+            int64_t tok = -1;
+            for (int32_t j = 0; j < V; ++j) {
+                int32_t i = idx_of(order[j]);
+                if (!surv[i]) continue;
+                incl += weight_of(e[i]);
+                if (incl > t) { tok = i; break; }
+            }
+            a->tokens[r] = tok;
+            if (a->kept) for (int32_t i = 0; i < V; ++i) a->kept[(int64_t)r * V + i] = surv[i];
+            if (a->probs) {
+                for (int32_t i = 0; i < V; ++i)
+                    a->probs[(int64_t)r * V + i] =
+                        surv[i] ? (float)((double)e[i] * 1099511627776.0 / (double)T) : 0.0f;
+            }
+        }
+        /* _logprobs, sampler.py:262-291, rule (R7) */
+        if (a->logprobs[r] >= 0) {
+            double lse = log((double)sall / 1099511627776.0);
+            if (a->chosen_lp) {
+                int64_t c = a->tokens[r];
+                a->chosen_lp[r] = (float)(((double)y[c] - (double)M) - lse);
+            }
+            if (a->top_ids) {
+                for (int32_t j = 0; j < a->lp_cols; ++j) {
+                    int64_t o = (int64_t)r * a->lp_cols + j;
+                    if (j < a->logprobs[r] && j < V) {
+                        int32_t i = idx_of(order[j]);
+                        a->top_ids[o] = i;
+                        a->top_lp[o] = (float)(((double)y[i] - (double)M) - lse);
+                    } else {
+                        a->top_ids[o] = -1;
+                        a->top_lp[o] = 0.0f;
+                    }
+                }
+            }
+        }
+    }
+    free(y); free(e); free(order); free(surv);
+    return 0;
+}
