@@ -98,6 +98,31 @@ FIE_DEV uint64_t floor_mul_f64(double u, uint64_t T)
     return (uint64_t)(prod >> q);
 }
 
+// ---------------------------------------------------------------- coherence
+// Workgroups of one pass hand results to the row's last workgroup without an
+// agent-scope fence (which writes back and invalidates the whole L2 of an XCD):
+// every value crossing workgroups is an agent-scope atomic (RMW, or a load/store
+// with the sc1 coherence bit), and a writer drains its memory counters before it
+// signals arrival, which orders those accesses the way the release fence would.
+template <typename T>
+FIE_DEV T ld_shared(const T* p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+FIE_DEV void st_shared(T* p, T v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+FIE_DEV void drain_memory()
+{
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // ---------------------------------------------------------------- reductions
 FIE_DEV uint64_t shfl_u64(uint64_t v, int src)
 {

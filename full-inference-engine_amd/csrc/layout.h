@@ -31,22 +31,21 @@ enum : uint32_t { kKindGreedy = 0, kKindTopK = 1, kKindWide = 2 };
 // Per-row state.  Accumulators are zero between calls: whoever consumes one
 // (the last workgroup of a pass) restores it to zero.
 struct RowState {
-    unsigned long long maxpack;      // pass 1: max of (wkey << 32 | ~index)
-    unsigned int minkey_inv;         // pass 1: max of ~wkey
-    unsigned int arrive[3];          // workgroups finished, per pass
-    unsigned long long sall;         // pass 2: sum of weights over the row
+    unsigned long long maxpack;      // max of (wkey << 32 | ~index) over the row
+    unsigned long long sall;         // sum of integer weights over the row
+    unsigned long long thr;          // ceil(p * S), the top-p threshold
+    unsigned long long S;            // survivor mass
+    unsigned long long Awa;          // survivor mass in front of window 0
+    unsigned long long Abc;          // survivor mass in front of the cut bin
+    unsigned int minkey_inv;         // max of ~wkey (the row minimum)
+    unsigned int arrive[3];          // workgroup arrivals per hand-off (+ kPlanReady)
     unsigned int nA, nB;             // candidates gathered
-    // written by the plans
-    unsigned int mode2, mode3;
-    float M, dscale;
-    unsigned int keyA;
-    int kk;
-    unsigned int wlo[2], whi[2];
-    int bc, nwin;
-    int argmax, kind;
-    unsigned int nA_kept, overflow;
-    unsigned long long thr, S;
-    unsigned long long pad;
+    float M, dscale;                 // row max of y; d-bin scale
+    unsigned int keyA;               // rank candidates: w-key lower bound
+    unsigned int wlo[2], whi[2];     // mass windows as w-key intervals
+    int bc, nwin, wb0;               // cut bin, windows, last bin of window 0
+    unsigned int overflow;
+    unsigned int pad[3];
 };
 static_assert(sizeof(RowState) == 128, "RowState is 128 bytes");
 

@@ -1,24 +1,20 @@
 // MI355X fused token sampler: kernels and the C ABI (include/fie_sampler.h).
 //
-// One sampler step for [rows, vocab] logits is a fixed chain of at most four
-// launches on the caller's stream, with no host synchronisation:
+// One sampler step for [rows, vocab] logits is at most two launches on the
+// caller's stream, with no host synchronisation:
 //
 //   k_penalty  (rows with penalties)  sampler.py:120-175: per-row distinct history
 //              ids, counts and penalised values, sorted by token id, cut into one
 //              segment per slice of the row.
-//   k_pass1    every (row, slice)     read #1 of the logits.  Applies the slice's
-//              penalty patches from LDS, tracks max/argmax/min of the penalised
-//              logit w, and for rows that need a rank selection a histogram of the
-//              order key of w.  The last workgroup of a row plans the row.
-//   k_pass2    rows not yet finished  read #2.  Top-k rows gather every token at or
-//              above the histogram bin of their k-th value; wide rows (sampled, no
-//              top-k) compute each token's integer weight and a mass histogram
-//              over d = y - M.  The last workgroup finishes top-k and greedy rows
-//              (sort the candidates, filters, draw) or plans the wide row's
-//              top-p cut and draw windows.
-//   k_pass3    wide rows              gathers the tokens inside the windows (a
-//              cheap key compare per element, no arithmetic); the last workgroup
-//              resolves the exact cut and draw.
+//   k_sample   one workgroup per (row, slice).  The slice is read from HBM once
+//              into registers, with the slice's penalty patches applied from LDS.
+//              Greedy rows need only the row max.  Top-k rows count the keys that
+//              can reach the top k into a histogram, agree on the bin of the k-th
+//              value and gather every token from that bin up.  Wide rows (sampled,
+//              no top-k) agree on the row max, weigh every token exactly, agree on
+//              the top-p cut and draw windows from the survivor mass histogram,
+//              and gather the tokens in those windows.  The row's last workgroup
+//              sorts the candidates and applies the filters and the draw.
 //
 // All mass sums are 64-bit integer sums of floor(cexp(y - M) * 2^40), so results
 // do not depend on how the row is split into workgroups or on atomic order.
@@ -27,6 +23,7 @@
 #include <stdint.h>
 #include <stdio.h>
 #include <string.h>
+#include <stdlib.h>
 
 #include "common.h"
 #include "layout.h"
@@ -184,12 +181,12 @@ FIE_DEV void apply_patches(const PatchView& pv, const PatchLds& L, int64_t e0, f
 {
     if (pv.n == 0) return;
     const int off = (int)(e0 - pv.e0);
-    uint32_t bits = (L.bitmap[off >> 5] >> (off & 31)) & ((1u << EPC) - 1u);
-    while (bits) {
-        const int j = __builtin_ctz(bits);
-        bits &= bits - 1;
-        v[j] = patch_value(pv, L, off + j);
-    }
+    const uint32_t bits = (L.bitmap[off >> 5] >> (off & 31)) & ((1u << EPC) - 1u);
+    if (bits == 0) return;
+    // static element indices only, so v[] stays in registers
+#pragma unroll
+    for (int j = 0; j < EPC; ++j)
+        if (bits & (1u << j)) v[j] = patch_value(pv, L, off + j);
 }
 
 // Calls f(w, index) for every element of slice s of row r, 16-byte chunks
@@ -238,23 +235,6 @@ FIE_DEV void for_each_element(const Params& P, int r, int s, const PatchView& pv
     }
 }
 
-// Arrival counter of the row for one pass.  Returns true in the last workgroup,
-// which then sees every other workgroup's global writes of that pass.
-FIE_DEV bool last_to_arrive(RowState& st, int pass, int S, int* flag)
-{
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        unsigned int old = atomicAdd(&st.arrive[pass], 1u);
-        *flag = (old == (unsigned int)(S - 1));
-        if (*flag) st.arrive[pass] = 0;
-    }
-    __syncthreads();
-    const bool last = *flag != 0;
-    if (last) __threadfence();
-    return last;
-}
-
 // Wave-aggregated append of (w bits, index) to a row's candidate buffer.
 FIE_DEV void append_candidate(bool pred, float w, uint32_t idx, unsigned int* counter,
                               uint64_t* buf)
@@ -269,7 +249,7 @@ FIE_DEV void append_candidate(bool pred, float w, uint32_t idx, unsigned int* co
     if (pred) {
         const unsigned int pos = base + (unsigned int)__popcll(mask & ((1ull << lane) - 1ull));
         if (pos < (unsigned int)kCap)
-            buf[pos] = ((uint64_t)__float_as_uint(w) << 32) | idx;
+            st_shared(&buf[pos], ((uint64_t)__float_as_uint(w) << 32) | idx);
     }
 }
 
@@ -350,7 +330,7 @@ __global__ __launch_bounds__(kPenThreads) void k_penalty(Params P)
     const int nvalid = (words > 0) ? (int)(prefix[words - 1] + __popc(bits[words - 1])) : 0;
     uint32_t* cnt = P.pen_cnt + off;
     for (int i = tid; i < nvalid; i += kPenThreads) cnt[i] = 0;
-    __threadfence();
+    drain_memory();
     __syncthreads();
     for (int64_t j = tid; j < n; j += kPenThreads) {
         const int id = ids[j];
@@ -359,7 +339,7 @@ __global__ __launch_bounds__(kPenThreads) void k_penalty(Params P)
             atomicAdd(&cnt[rk], 1u);
         }
     }
-    __threadfence();
+    drain_memory();
     __syncthreads();
     // penalised values in token-id order (sampler.py:169-173)
     const char* row = row_ptr(P, r);
@@ -420,181 +400,200 @@ __global__ __launch_bounds__(kPenThreads) void k_penalty(Params P)
     }
 }
 
-// ============================================================== pass 1
-struct Pass1Lds {
-    PatchLds patch;
-    uint32_t hist[kCountBins];
-    uint64_t red[kWaves + 1];
-    int flag;
-    int found_bin;
-};
+// ============================================================== row hand-off
+// The workgroups of one row cooperate through three arrival counters in the
+// row's state.  A workgroup publishes its partial results (agent-scope atomics),
+// drains its memory counters and increments the counter; the last one to arrive
+// turns the merged partials into a plan, publishes it and raises kPlanReady;
+// the others wait for that bit.  The wait is bounded: a workgroup that gives up
+// marks the row FIE_ROW_TIMEOUT and leaves, and the host resolves such a row
+// with the exact fallback.  Waiting is safe because workgroups are dispatched in
+// order and one row's workgroups are consecutive, so a row never waits on a
+// workgroup that cannot become resident.
+constexpr unsigned int kPlanReady = 0x80000000u;
+constexpr unsigned int kSpinLimit = 1u << 18;
 
-FIE_DEV bool wants_rank_select(const Params& P, int r)
+FIE_DEV bool arrive(unsigned int* ctr, int S, int* flag)
 {
-    const bool greedy = P.flags[r] & 1;
-    return (!greedy && P.top_k[r] > 0) || P.logprobs[r] > 0;
+    drain_memory();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned int old = atomicAdd(ctr, 1u);
+        *flag = ((old & ~kPlanReady) == (unsigned int)(S - 1));
+    }
+    __syncthreads();
+    return *flag != 0;
 }
 
+FIE_DEV void publish_plan(unsigned int* ctr)
+{
+    drain_memory();
+    __syncthreads();
+    if (threadIdx.x == 0) atomicOr(ctr, kPlanReady);
+}
+
+FIE_DEV bool wait_plan(unsigned int* ctr, int* flag)
+{
+    if (threadIdx.x == 0) {
+        unsigned int n = 0;
+        bool ok = true;
+        while (!(ld_shared(ctr) & kPlanReady)) {
+            __builtin_amdgcn_s_sleep(2);
+            if (++n > kSpinLimit) { ok = false; break; }
+        }
+        *flag = ok;
+    }
+    __syncthreads();
+    return *flag != 0;
+}
+
+// ============================================================== per-row plans
 FIE_DEV void write_row_outputs_default(const Params& P, int r)
 {
-    P.status[r] = 0;
     P.tk_key[r] = 0;
     P.cut_comp[r] = 0;
     P.kept_mass[r] = 0;
     P.row_mass[r] = 0;
 }
 
-FIE_DEV void plan1(const Params& P, int r, Pass1Lds& L)
-{
-    RowState& st = P.st[r];
-    const unsigned long long mp = st.maxpack;
-    const unsigned int minv = st.minkey_inv;
-    const int tid = threadIdx.x;
-    __syncthreads();
-    const int argmax = (int)(0xFFFFFFFFu - (uint32_t)(mp & 0xFFFFFFFFu));
-    if (P.argmax_only) {
-        if (tid == 0) {
-            st.maxpack = 0;
-            st.minkey_inv = 0;
-            P.tokens[r] = argmax;
-        }
-        return;
-    }
-    const bool greedy = P.flags[r] & 1;
-    const int k = greedy ? 0 : P.top_k[r];
-    const int Lp = P.logprobs[r];
-    const float s = P.scale[r];
-    const float wmax = key_to_float((uint32_t)(mp >> 32));
-    const float M = scaled(wmax, s);
-    uint32_t mode2 = 0;
-    int kk = 0;
-    if (wants_rank_select(P, r)) {
-        kk = k > Lp ? k : Lp;
-        if (kk > P.vocab) kk = P.vocab;
-        // bins of the global histogram, 16 per thread, descending from the top
-        uint32_t* gh = P.chist + (int64_t)r * kCountBins;
-        constexpr int per = kCountBins / kThreads;
-        const int bhi = kCountBins - 1 - tid * per;
-        uint32_t c[per];
-        uint64_t local = 0;
-#pragma unroll
-        for (int i = 0; i < per; ++i) {
-            c[i] = gh[bhi - i];
-            gh[bhi - i] = 0;
-            local += c[i];
-        }
-        uint64_t total;
-        uint64_t above = block_excl_scan_u64<kThreads>(local, L.red, &total);
-        if (tid == 0) L.found_bin = 0;
-        __syncthreads();
-        if (above < (uint64_t)kk && above + local >= (uint64_t)kk) {
-            uint64_t cum = above;
-            for (int i = 0; i < per; ++i) {
-                cum += c[i];
-                if (cum >= (uint64_t)kk) { L.found_bin = bhi - i; break; }
-            }
-        }
-        __syncthreads();
-        mode2 |= kM2CollectA;
-    }
-    if (tid == 0) {
-        st.maxpack = 0;
-        st.minkey_inv = 0;
-        st.M = M;
-        st.argmax = argmax;
-        st.kk = kk;
-        st.nA = 0;
-        st.nB = 0;
-        st.overflow = 0;
-        if (mode2 & kM2CollectA) {
-            const int64_t lo = ((int64_t)L.found_bin << kCountShift) - 16;
-            st.keyA = lo > 0 ? (uint32_t)lo : 0u;
-        }
-        if (Lp >= 0) mode2 |= kM2Weights;
-        int kind = greedy ? kKindGreedy : (k > 0 ? kKindTopK : kKindWide);
-        if (kind == kKindWide) {
-            mode2 |= kM2Weights | kM2MassHist;
-            const float ymin = scaled(key_to_float(~minv), s);
-            float R = fminf(M - ymin, 28.0f);
-            st.dscale = (R > 0.0f) ? (float)(kMassBins - 1) / R : 0.0f;
-        }
-        st.kind = kind;
-        st.mode2 = mode2;
-        st.mode3 = 0;
-        P.row_max[r] = M;
-        if (mode2 == 0) {
-            // greedy without logprobs: the argmax is the answer (sampler.py:236-238)
-            write_row_outputs_default(P, r);
-            P.kept_mass[r] = weight_of(1.0f);
-            P.tokens[r] = argmax;
-        }
-    }
-}
-
-template <int DT>
-__global__ __launch_bounds__(kThreads) void k_pass1(Params P)
-{
-    __shared__ Pass1Lds L;
-    const int r = blockIdx.x / P.S, s = blockIdx.x % P.S;
-    RowState& st = P.st[r];
-    const bool want_hist = !P.argmax_only && wants_rank_select(P, r);
-    for (int i = threadIdx.x; i < kCountBins && want_hist; i += kThreads) L.hist[i] = 0;
-    const PatchView pv = stage_patches(P, r, s, L.patch);
-    __syncthreads();
-    uint64_t best = 0;
-    uint32_t minv = 0;
-    for_each_element<DT>(P, r, s, pv, L.patch, [&](float w, uint32_t idx) {
-        const uint32_t k = fkey(w + 0.0f);
-        const uint64_t pack = ((uint64_t)k << 32) | (0xFFFFFFFFu - idx);
-        best = pack > best ? pack : best;
-        minv = (~k) > minv ? ~k : minv;
-        if (want_hist) atomicAdd(&L.hist[k >> kCountShift], 1u);
-    });
-    best = block_max_u64<kThreads>(best, L.red);
-    minv = (uint32_t)block_max_u64<kThreads>(minv, L.red);
-    if (threadIdx.x == 0) {
-        atomicMax(&st.maxpack, (unsigned long long)best);
-        atomicMax(&st.minkey_inv, minv);
-    }
-    if (want_hist) {
-        __syncthreads();
-        uint32_t* gh = P.chist + (int64_t)r * kCountBins;
-        for (int i = threadIdx.x; i < kCountBins; i += kThreads)
-            if (L.hist[i]) atomicAdd(&gh[i], L.hist[i]);
-    }
-    if (!last_to_arrive(st, 0, P.S, &L.flag)) return;
-    plan1(P, r, L);
-}
-
-// ============================================================== pass 2
-struct FinLds {
-    uint64_t key[kCap];
-    uint64_t wt[kCap];
-    uint64_t red[kWaves + 1];
-    uint64_t scal[8];
-};
-
-struct PlanPLds {
-    uint64_t A[kMassBins + 1];
-    uint32_t cnt[kMassBins];
-    uint64_t red[kWaves + 1];
-    int ints[16];
-};
-
-struct Pass2Stream {
+struct SampleLds {
     PatchLds patch;
-    uint32_t cnt[kMassBins];
-    unsigned long long mass[kMassBins];
+    union {
+        uint32_t chist[kCountBins];
+        struct {
+            uint32_t cnt[kMassBins];
+            unsigned long long mass[kMassBins];
+        } mh;
+        uint64_t key[kCap];
+    } u;
+    uint64_t red[kWaves + 1];
+    uint64_t scal[4];
+    uint32_t ured[kWaves];
+    int flag;
+    int found_bin;
 };
 
-union Pass2Lds {
-    Pass2Stream str;
-    FinLds fin;
-    PlanPLds plan;
-};
+// Rank selection of the row (top-k and logprob lists): the bin of the global
+// count histogram that holds the kk-th largest w; candidates are gathered from
+// that bin's lower edge (less a margin that covers values a temperature divide
+// merges with the threshold value).
+FIE_DEV uint32_t plan_rank(const Params& P, int r, int kk, SampleLds& L)
+{
+    uint32_t* gh = P.chist + (int64_t)r * kCountBins;
+    constexpr int per = kCountBins / kThreads;
+    const int tid = threadIdx.x;
+    const int bhi = kCountBins - 1 - tid * per;
+    uint32_t c[per];
+    uint64_t local = 0;
+#pragma unroll
+    for (int i = 0; i < per; ++i) {
+        c[i] = ld_shared(&gh[bhi - i]);
+        if (c[i]) st_shared(&gh[bhi - i], 0u);
+        local += c[i];
+    }
+    uint64_t total;
+    const uint64_t above = block_excl_scan_u64<kThreads>(local, L.red, &total);
+    if (tid == 0) L.found_bin = 0;
+    __syncthreads();
+    if (above < (uint64_t)kk && above + local >= (uint64_t)kk) {
+        uint64_t cum = above;
+        for (int i = 0; i < per; ++i) {
+            cum += c[i];
+            if (cum >= (uint64_t)kk) { L.found_bin = bhi - i; break; }
+        }
+    }
+    __syncthreads();
+    const int64_t lo = ((int64_t)L.found_bin << kCountShift) - 16;
+    return lo > 0 ? (uint32_t)lo : 0u;
+}
 
-// Top-L logprob entries of a row from its sorted candidates (sampler.py:273-291:
-// chosen first, then the best alternatives; the host drops the chosen one).
+// Wide rows: from the survivor mass histogram, the bin holding the top-p cut
+// (first bin whose inclusive mass reaches ceil(p*S)) and the bins the draw can
+// land in, as at most two w-key intervals; run by the row's last workgroup.
+FIE_DEV void plan_wide(const Params& P, int r, SampleLds& L)
+{
+    RowState& st = P.st[r];
+    const int tid = threadIdx.x;
+    unsigned long long* gm = P.mmass + (int64_t)r * kMassBins;
+    uint32_t* gc = P.mcnt + (int64_t)r * kMassBins;
+    constexpr int per = kMassBins / kThreads;
+    const int b0 = tid * per;
+    uint64_t m[per];
+    uint64_t local = 0;
+#pragma unroll
+    for (int i = 0; i < per; ++i) {
+        m[i] = ld_shared(&gm[b0 + i]);
+        L.u.mh.cnt[b0 + i] = ld_shared(&gc[b0 + i]);
+        local += m[i];
+    }
+    uint64_t S;
+    uint64_t run = block_excl_scan_u64<kThreads>(local, L.red, &S);
+    unsigned long long* A = L.u.mh.mass;   // A[b] = survivor mass of bins < b
+#pragma unroll
+    for (int i = 0; i < per; ++i) { A[b0 + i] = run; run += m[i]; }
+    __syncthreads();
+    const float p = P.top_p[r];
+    const double u = P.uniform[r];
+    if (tid == 0) {
+        auto Aat = [&](int b) -> uint64_t { return b >= kMassBins ? S : A[b]; };
+        int bc = -1, blo, bhi;
+        uint64_t thr = ~0ull;
+        if (p < 1.0f) {
+            thr = ceil_mul_f32(p, S);
+            int lo = 0, hi = kMassBins - 1;
+            while (lo < hi) { int mid = (lo + hi) >> 1; if (Aat(mid + 1) >= thr) hi = mid; else lo = mid + 1; }
+            bc = lo;
+            const uint64_t tlo = floor_mul_f64(u, Aat(bc));
+            const uint64_t thi = floor_mul_f64(u, Aat(bc + 1));
+            lo = 0; hi = bc;
+            while (lo < hi) { int mid = (lo + hi) >> 1; if (Aat(mid + 1) > tlo) hi = mid; else lo = mid + 1; }
+            blo = lo;
+            lo = 0; hi = bc;
+            while (lo < hi) { int mid = (lo + hi) >> 1; if (Aat(mid + 1) > thi) hi = mid; else lo = mid + 1; }
+            bhi = lo;
+        } else {
+            const uint64_t t = floor_mul_f64(u, S);
+            int lo = 0, hi = kMassBins - 1;
+            while (lo < hi) { int mid = (lo + hi) >> 1; if (Aat(mid + 1) > t) hi = mid; else lo = mid + 1; }
+            blo = bhi = lo;
+        }
+        int wa[2] = {blo, 0}, wb[2] = {bhi, 0}, nw = 1;
+        if (bc >= 0 && bc > bhi) {
+            if (bc == bhi + 1) wb[0] = bc;
+            else { wa[1] = bc; wb[1] = bc; nw = 2; }
+        }
+        uint64_t count = 0;
+        for (int w = 0; w < nw; ++w)
+            for (int b = wa[w]; b <= wb[w]; ++b) count += L.u.mh.cnt[b];
+        const float s = P.scale[r], M = ld_shared(&st.M), ds = ld_shared(&st.dscale);
+        for (int w = 0; w < nw; ++w) {
+            uint32_t lo2 = kKeyNegInf, hi2 = kKeyPosInf;
+            while (lo2 < hi2) {       // smallest key with bin <= wb
+                const uint32_t mid = lo2 + (hi2 - lo2) / 2;
+                if (bin_of_key(mid, s, M, ds) <= wb[w]) hi2 = mid; else lo2 = mid + 1;
+            }
+            st_shared(&st.wlo[w], lo2);
+            lo2 = kKeyNegInf; hi2 = kKeyPosInf;
+            while (lo2 < hi2) {       // largest key with bin >= wa
+                const uint32_t mid = lo2 + (hi2 - lo2 + 1) / 2;
+                if (bin_of_key(mid, s, M, ds) >= wa[w]) lo2 = mid; else hi2 = mid - 1;
+            }
+            st_shared(&st.whi[w], lo2);
+        }
+        st_shared(&st.nwin, nw);
+        st_shared(&st.bc, bc);
+        st_shared(&st.wb0, wb[0]);
+        st_shared(&st.thr, (unsigned long long)thr);
+        st_shared(&st.S, (unsigned long long)S);
+        st_shared(&st.Awa, (unsigned long long)Aat(wa[0]));
+        st_shared(&st.Abc, (unsigned long long)(bc >= 0 ? Aat(bc) : 0));
+        if (count > (uint64_t)kCap) atomicOr(&st.overflow, 1u);
+    }
+    __syncthreads();
+}
+
+// ============================================================== finishing a row
+// Top-L logprob entries from sorted candidates (sampler.py:273-291).
 FIE_DEV void write_logprobs(const Params& P, int r, const uint64_t* key, int n, float M,
                             uint64_t sall, float ychosen)
 {
@@ -616,14 +615,15 @@ FIE_DEV void write_logprobs(const Params& P, int r, const uint64_t* key, int n, 
     }
 }
 
-// Loads n candidates (w bits, index), converts to rank keys of y and sorts them.
-FIE_DEV int load_sorted(const uint64_t* buf, int n, float s, uint64_t* key)
+// Loads n candidates (w bits, index), turns them into rank keys of y and sorts
+// them (value descending, index ascending).
+FIE_DEV void load_sorted(const uint64_t* buf, int n, float s, uint64_t* key)
 {
     const int N = pow2_at_least(n);
     for (int i = threadIdx.x; i < N; i += kThreads) {
         uint64_t c = 0;
         if (i < n) {
-            const uint64_t raw = buf[i];
+            const uint64_t raw = ld_shared(&buf[i]);
             const float y = scaled(__uint_as_float((uint32_t)(raw >> 32)), s);
             c = comp_key(fkey(y), (uint32_t)raw);
         }
@@ -631,49 +631,53 @@ FIE_DEV int load_sorted(const uint64_t* buf, int n, float s, uint64_t* key)
     }
     __syncthreads();
     bitonic_sort_desc<kThreads>(key, N);
-    return N;
 }
 
-// Filters and draw over candidates that hold every survivor (greedy and top-k
-// rows): sampler.py:194-228 with rules (R2)-(R5), then the draw (R4).
-FIE_DEV void finalize_topk(const Params& P, int r, FinLds& L)
+FIE_DEV void set_status(const Params& P, int r, int bits)
+{
+    if (bits) atomicOr(&P.status[r], bits);
+}
+
+// Greedy rows with logprobs and top-k rows: the candidates hold every survivor.
+// Filters sampler.py:194-228 with rules R2-R5, then the draw R4.
+FIE_DEV void finalize_topk(const Params& P, int r, int kind, SampleLds& L)
 {
     RowState& st = P.st[r];
     const int tid = threadIdx.x;
-    const int kind = st.kind;
-    const float s = P.scale[r], M = st.M;
-    const unsigned int nraw = st.nA;
+    const float s = P.scale[r], M = ld_shared(&st.M);
+    const unsigned int nraw = ld_shared(&st.nA);
     const bool over = nraw > (unsigned int)kCap;
     const int n = over ? kCap : (int)nraw;
-    const uint64_t sall = st.sall;
-    __syncthreads();
-    if (tid == 0) { st.nA = 0; st.sall = 0; }
+    const uint64_t sall = ld_shared(&st.sall);
+    const uint32_t keyA = ld_shared(&st.keyA);
+    uint64_t* key = L.u.key;
     if (kind == kKindGreedy) {
-        if (P.logprobs[r] > 0) load_sorted(P.candA + (int64_t)r * kCap, n, s, L.key);
-        write_logprobs(P, r, L.key, n, M, sall, M);
+        const unsigned long long mp = ld_shared(&st.maxpack);
+        const int argmax = (int)(0xFFFFFFFFu - (uint32_t)(mp & 0xFFFFFFFFu));
+        if (P.logprobs[r] > 0) load_sorted(P.candA + (int64_t)r * kCap, n, s, key);
+        write_logprobs(P, r, key, n, M, sall, M);
         if (tid == 0) {
             write_row_outputs_default(P, r);
-            P.status[r] = over ? FIE_ROW_OVERFLOW : 0;
+            set_status(P, r, over ? FIE_ROW_OVERFLOW : 0);
             P.kept_mass[r] = weight_of(1.0f);
-            P.row_mass[r] = (st.mode2 & kM2Weights) ? sall : 0;
-            P.tokens[r] = st.argmax;
+            P.row_mass[r] = sall;
+            P.tokens[r] = argmax;
         }
         return;
     }
-    const int N = load_sorted(P.candA + (int64_t)r * kCap, n, s, L.key);
-    (void)N;
+    load_sorted(P.candA + (int64_t)r * kCap, n, s, key);
     const int k = P.top_k[r];
     const float mp = P.min_p[r];
     const float p = P.top_p[r];
-    const uint32_t tk = (k >= 1 && k <= n) ? (uint32_t)(L.key[k - 1] >> 32) : 0u;
-    // Survivors outside the candidate set would have w-key < keyA; check that the
+    const uint32_t tk = (k >= 1 && k <= n) ? (uint32_t)(key[k - 1] >> 32) : 0u;
+    // A survivor outside the candidates would have w-key < keyA: check that the
     // largest such value cannot reach the threshold.
     bool unsafe = over || k > n;
-    if (st.keyA > kKeyNegInf) {
-        const float yout = scaled(key_to_float(st.keyA - 1), s);
+    if (keyA > kKeyNegInf) {
+        const float yout = scaled(key_to_float(keyA - 1), s);
         if (fkey(yout) >= tk) unsafe = true;
     }
-    constexpr int per = kCap / kThreads;  // contiguous positions per thread
+    constexpr int per = kCap / kThreads;
     const int j0 = tid * per;
     uint64_t w[per];
     bool sv[per];
@@ -684,8 +688,7 @@ FIE_DEV void finalize_topk(const Params& P, int r, FinLds& L)
         sv[i] = false;
         w[i] = 0;
         if (j < n) {
-            const uint64_t c = L.key[j];
-            const uint32_t yk = (uint32_t)(c >> 32);
+            const uint32_t yk = (uint32_t)(key[j] >> 32);
             const float e = cexp(key_to_float(yk) - M);
             sv[i] = yk >= tk && !(mp > 0.0f && e < mp);
             if (sv[i]) w[i] = weight_of(e);
@@ -700,7 +703,7 @@ FIE_DEV void finalize_topk(const Params& P, int r, FinLds& L)
 #pragma unroll
     for (int i = 0; i < per; ++i) {
         kept[i] = sv[i] && ex < thr;
-        if (kept[i]) { kept_local += w[i]; cut = L.key[j0 + i] < cut ? L.key[j0 + i] : cut; }
+        if (kept[i]) { kept_local += w[i]; cut = key[j0 + i] < cut ? key[j0 + i] : cut; }
         ex += w[i];
     }
     const uint64_t T = block_sum_u64<kThreads>(kept_local, L.red);
@@ -711,235 +714,42 @@ FIE_DEV void finalize_topk(const Params& P, int r, FinLds& L)
     ex = excl0;
 #pragma unroll
     for (int i = 0; i < per; ++i) {
-        if (kept[i] && ex <= t && t < ex + w[i]) L.scal[0] = L.key[j0 + i];
+        if (kept[i] && ex <= t && t < ex + w[i]) L.scal[0] = key[j0 + i];
         ex += w[i];
     }
     __syncthreads();
     const uint64_t chosen = L.scal[0];
-    const float ych = key_to_float((uint32_t)(chosen >> 32));
-    write_logprobs(P, r, L.key, n, M, sall, ych);
+    write_logprobs(P, r, key, n, M, sall, key_to_float((uint32_t)(chosen >> 32)));
     if (tid == 0) {
-        write_row_outputs_default(P, r);
-        P.status[r] = (unsafe || chosen == ~0ull) ? FIE_ROW_OVERFLOW : 0;
+        set_status(P, r, (unsafe || chosen == ~0ull) ? FIE_ROW_OVERFLOW : 0);
         P.tk_key[r] = tk;
         P.cut_comp[r] = (p < 1.0f && cut != ~0ull) ? cut : 0;
         P.kept_mass[r] = T;
-        P.row_mass[r] = (st.mode2 & kM2Weights) ? sall : 0;
+        P.row_mass[r] = (P.logprobs[r] >= 0) ? sall : 0;
         P.tokens[r] = (chosen == ~0ull) ? -1 : (int64_t)comp_idx(chosen);
     }
 }
 
-// Wide rows after pass 2: the survivor mass histogram decides the bin holding the
-// top-p cut (first bin whose inclusive mass reaches ceil(p*S)) and the bins the
-// draw can land in; pass 3 gathers exactly those bins.
-FIE_DEV void plan_wide(const Params& P, int r, PlanPLds& L)
+// Wide rows: exact cut and draw from the window candidates and the masses in
+// front of the windows (rules R2-R4).
+FIE_DEV void finalize_wide(const Params& P, int r, SampleLds& L)
 {
     RowState& st = P.st[r];
     const int tid = threadIdx.x;
-    const unsigned long long* gm = P.mmass + (int64_t)r * kMassBins;
-    const uint32_t* gc = P.mcnt + (int64_t)r * kMassBins;
-    constexpr int per = kMassBins / kThreads;
-    const int b0 = tid * per;
-    uint64_t m[per];
-    uint64_t local = 0;
-#pragma unroll
-    for (int i = 0; i < per; ++i) {
-        m[i] = gm[b0 + i];
-        L.cnt[b0 + i] = gc[b0 + i];
-        local += m[i];
-    }
-    uint64_t S;
-    uint64_t run = block_excl_scan_u64<kThreads>(local, L.red, &S);
-#pragma unroll
-    for (int i = 0; i < per; ++i) { L.A[b0 + i] = run; run += m[i]; }
-    if (tid == 0) L.A[kMassBins] = S;
-    __syncthreads();
-    const float p = P.top_p[r];
-    const double u = P.uniform[r];
-    if (tid == 0) {
-        int bc = -1, blo, bhi;
-        uint64_t thr = ~0ull;
-        if (p < 1.0f) {
-            thr = ceil_mul_f32(p, S);
-            // first bin whose inclusive cumulative mass reaches thr
-            int lo = 0, hi = kMassBins - 1;
-            while (lo < hi) { int mid = (lo + hi) >> 1; if (L.A[mid + 1] >= thr) hi = mid; else lo = mid + 1; }
-            bc = lo;
-            const uint64_t tlo = floor_mul_f64(u, L.A[bc]);
-            const uint64_t thi = floor_mul_f64(u, L.A[bc + 1]);
-            lo = 0; hi = bc;
-            while (lo < hi) { int mid = (lo + hi) >> 1; if (L.A[mid + 1] > tlo) hi = mid; else lo = mid + 1; }
-            blo = lo;
-            lo = 0; hi = bc;
-            while (lo < hi) { int mid = (lo + hi) >> 1; if (L.A[mid + 1] > thi) hi = mid; else lo = mid + 1; }
-            bhi = lo;
-        } else {
-            const uint64_t t = floor_mul_f64(u, S);
-            int lo = 0, hi = kMassBins - 1;
-            while (lo < hi) { int mid = (lo + hi) >> 1; if (L.A[mid + 1] > t) hi = mid; else lo = mid + 1; }
-            blo = bhi = lo;
-        }
-        // windows as bin ranges, bins ascending = values descending
-        int wa[2], wb[2], nw = 1;
-        wa[0] = blo; wb[0] = bhi;
-        if (bc >= 0 && bc > bhi) {
-            if (bc == bhi + 1) wb[0] = bc;
-            else { wa[1] = bc; wb[1] = bc; nw = 2; }
-        }
-        uint64_t count = 0;
-        for (int w = 0; w < nw; ++w)
-            for (int b = wa[w]; b <= wb[w]; ++b) count += L.cnt[b];
-        const float s = P.scale[r], M = st.M, ds = st.dscale;
-        // bins -> w-key intervals (bin index is non-increasing in the key)
-        for (int w = 0; w < nw; ++w) {
-            uint32_t lo2 = kKeyNegInf, hi2 = kKeyPosInf;
-            while (lo2 < hi2) {       // smallest key with bin <= wb
-                uint32_t mid = lo2 + (hi2 - lo2) / 2;
-                if (bin_of_key(mid, s, M, ds) <= wb[w]) hi2 = mid; else lo2 = mid + 1;
-            }
-            st.wlo[w] = lo2;
-            lo2 = kKeyNegInf; hi2 = kKeyPosInf;
-            while (lo2 < hi2) {       // largest key with bin >= wa
-                uint32_t mid = lo2 + (hi2 - lo2 + 1) / 2;
-                if (bin_of_key(mid, s, M, ds) >= wa[w]) lo2 = mid; else hi2 = mid - 1;
-            }
-            st.whi[w] = lo2;
-        }
-        st.nwin = nw;
-        st.bc = bc;
-        st.thr = thr;
-        st.S = S;
-        st.mode3 = kM3CollectB;
-        st.overflow = count > (uint64_t)kCap ? 1u : 0u;
-    }
-    __syncthreads();
-}
-
-template <int DT>
-__global__ __launch_bounds__(kThreads) void k_pass2(Params P)
-{
-    __shared__ Pass2Lds L;
-    __shared__ int s_flag;
-    __shared__ uint64_t s_red[kWaves + 1];
-    const int r = blockIdx.x / P.S, s = blockIdx.x % P.S;
-    RowState& st = P.st[r];
-    const uint32_t mode = st.mode2;
-    if (mode == 0) return;
-    const bool collect = mode & kM2CollectA;
-    const bool weights = mode & kM2Weights;
-    const bool hist = mode & kM2MassHist;
-    if (hist)
-        for (int i = threadIdx.x; i < kMassBins; i += kThreads) { L.str.cnt[i] = 0; L.str.mass[i] = 0; }
-    const PatchView pv = stage_patches(P, r, s, L.str.patch);
-    __syncthreads();
-    const uint32_t keyA = st.keyA;
-    const float sc = P.scale[r], M = st.M, ds = st.dscale, mp = P.min_p[r];
-    uint64_t* candA = P.candA + (int64_t)r * kCap;
-    uint64_t sall = 0;
-    for_each_element<DT>(P, r, s, pv, L.str.patch, [&](float w, uint32_t idx) {
-        if (collect) append_candidate(fkey(w + 0.0f) >= keyA, w, idx, &st.nA, candA);
-        if (weights) {
-            const float y = scaled(w, sc);
-            const float d = y - M;
-            const float e = cexp(d);
-            const uint64_t wt = weight_of(e);
-            sall += wt;
-            if (hist && !(mp > 0.0f && e < mp)) {
-                const int b = d_bin(d, ds);
-                atomicAdd(&L.str.cnt[b], 1u);
-                atomicAdd(&L.str.mass[b], (unsigned long long)wt);
-            }
-        }
-    });
-    if (weights) {
-        sall = block_sum_u64<kThreads>(sall, s_red);
-        if (threadIdx.x == 0) atomicAdd(&st.sall, (unsigned long long)sall);
-    }
-    if (hist) {
-        __syncthreads();
-        uint32_t* gc = P.mcnt + (int64_t)r * kMassBins;
-        unsigned long long* gm = P.mmass + (int64_t)r * kMassBins;
-        for (int i = threadIdx.x; i < kMassBins; i += kThreads) {
-            if (L.str.cnt[i]) {
-                atomicAdd(&gc[i], L.str.cnt[i]);
-                atomicAdd(&gm[i], L.str.mass[i]);
-            }
-        }
-    }
-    if (!last_to_arrive(st, 1, P.S, &s_flag)) return;
-    if (st.kind == kKindWide) {
-        plan_wide(P, r, L.plan);
-        if (threadIdx.x == 0) {
-            // keep the top-L candidates of pass 2 and the row mass for pass 3
-            st.nA_kept = st.nA;
-            st.nA = 0;
-        }
-    } else {
-        finalize_topk(P, r, L.fin);
-    }
-}
-
-// ============================================================== pass 3
-struct FinWideLds {
-    uint64_t key[kCap];
-    uint64_t wt[kCap];
-    uint64_t A[kMassBins + 1];
-    int first[kMassBins];
-    uint64_t red[kWaves + 1];
-    uint64_t scal[4];
-};
-
-union Pass3Lds {
-    PatchLds patch;
-    FinWideLds fin;
-    FinLds lp;
-};
-
-// Exact cut and draw of a wide row from the gathered window candidates and the
-// survivor mass histogram (rules R2-R4).
-FIE_DEV void finalize_wide(const Params& P, int r, FinWideLds& L)
-{
-    RowState& st = P.st[r];
-    const int tid = threadIdx.x;
-    const float s = P.scale[r], M = st.M, ds = st.dscale, p = P.top_p[r];
-    const unsigned int nraw = st.nB;
+    const float s = P.scale[r], p = P.top_p[r];
+    const float M = ld_shared(&st.M), ds = ld_shared(&st.dscale);
+    const unsigned int nraw = ld_shared(&st.nB);
     const int n = nraw > (unsigned int)kCap ? kCap : (int)nraw;
-    const int bc = st.bc;
-    const uint64_t thr = st.thr, S = st.S;
-    const bool over = st.overflow || nraw > (unsigned int)kCap;
-    const uint64_t sall = st.sall;
-    // survivor prefix masses per bin; clear the histograms for the next call
-    {
-        unsigned long long* gm = P.mmass + (int64_t)r * kMassBins;
-        uint32_t* gc = P.mcnt + (int64_t)r * kMassBins;
-        constexpr int per = kMassBins / kThreads;
-        const int b0 = tid * per;
-        uint64_t m[per];
-        uint64_t local = 0;
-#pragma unroll
-        for (int i = 0; i < per; ++i) {
-            m[i] = gm[b0 + i];
-            gm[b0 + i] = 0;
-            gc[b0 + i] = 0;
-            local += m[i];
-            L.first[b0 + i] = 0x7FFFFFFF;
-        }
-        uint64_t tot;
-        uint64_t run = block_excl_scan_u64<kThreads>(local, L.red, &tot);
-#pragma unroll
-        for (int i = 0; i < per; ++i) { L.A[b0 + i] = run; run += m[i]; }
-        if (tid == 0) L.A[kMassBins] = tot;
-    }
-    const int N = load_sorted(P.candB + (int64_t)r * kCap, n, s, L.key);
-    for (int j = tid; j < n; j += kThreads) {
-        const uint32_t yk = (uint32_t)(L.key[j] >> 32);
-        const float d = key_to_float(yk) - M;
-        atomicMin(&L.first[d_bin(d, ds)], j);
-    }
-    __syncthreads();
+    const int bc = ld_shared(&st.bc), wb0 = ld_shared(&st.wb0);
+    const uint64_t thr = ld_shared(&st.thr), S = ld_shared(&st.S);
+    const uint64_t Awa = ld_shared(&st.Awa), Abc = ld_shared(&st.Abc);
+    const bool over = ld_shared(&st.overflow) || nraw > (unsigned int)kCap;
+    const uint64_t sall = ld_shared(&st.sall);
+    uint64_t* key = L.u.key;
+    load_sorted(P.candB + (int64_t)r * kCap, n, s, key);
     constexpr int per = kCap / kThreads;
     const int j0 = tid * per;
-    uint64_t w[per];
+    uint64_t w[per], w0 = 0;
     int bn[per];
     uint64_t local = 0;
 #pragma unroll
@@ -948,18 +758,16 @@ FIE_DEV void finalize_wide(const Params& P, int r, FinWideLds& L)
         w[i] = 0;
         bn[i] = kMassBins;
         if (j < n) {
-            const float d = key_to_float((uint32_t)(L.key[j] >> 32)) - M;
+            const float d = key_to_float((uint32_t)(key[j] >> 32)) - M;
             w[i] = weight_of(cexp(d));
             bn[i] = d_bin(d, ds);
+            if (bn[i] <= wb0) w0 += w[i];
         }
         local += w[i];
     }
     uint64_t tot;
     uint64_t pre = block_excl_scan_u64<kThreads>(local, L.red, &tot);
-    // candidate prefix sums, then each candidate's exclusive mass in rank order
-#pragma unroll
-    for (int i = 0; i < per; ++i) { L.wt[j0 + i] = pre; pre += w[i]; }
-    __syncthreads();
+    const uint64_t W0 = block_sum_u64<kThreads>(w0, L.red);   // mass gathered in window 0
     uint64_t ex[per];
     bool kept[per];
     uint64_t kept_bc = 0, cut = ~0ull;
@@ -970,33 +778,33 @@ FIE_DEV void finalize_wide(const Params& P, int r, FinWideLds& L)
         ex[i] = 0;
         if (j < n) {
             const int b = bn[i];
-            ex[i] = L.A[b] + (L.wt[j] - L.wt[L.first[b]]);
+            ex[i] = (b <= wb0) ? Awa + pre : Abc + (pre - W0);
             if (p < 1.0f) {
                 kept[i] = b < bc || (b == bc && ex[i] < thr);
                 if (b == bc && kept[i]) {
                     kept_bc += w[i];
-                    cut = L.key[j] < cut ? L.key[j] : cut;
+                    cut = key[j] < cut ? key[j] : cut;
                 }
             } else {
                 kept[i] = true;
             }
         }
+        pre += w[i];
     }
     kept_bc = block_sum_u64<kThreads>(kept_bc, L.red);
     cut = block_min_u64<kThreads>(cut, L.red);
-    const uint64_t T = (p < 1.0f) ? L.A[bc] + kept_bc : S;
+    const uint64_t T = (p < 1.0f) ? Abc + kept_bc : S;
     const uint64_t t = floor_mul_f64(P.uniform[r], T);
     if (tid == 0) L.scal[0] = ~0ull;
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < per; ++i)
-        if (kept[i] && ex[i] <= t && t < ex[i] + w[i]) L.scal[0] = L.key[j0 + i];
+        if (kept[i] && ex[i] <= t && t < ex[i] + w[i]) L.scal[0] = key[j0 + i];
     __syncthreads();
     const uint64_t chosen = L.scal[0];
-    (void)N;
     if (tid == 0) {
-        write_row_outputs_default(P, r);
-        P.status[r] = (over || chosen == ~0ull) ? FIE_ROW_OVERFLOW : 0;
+        set_status(P, r, (over || chosen == ~0ull) ? FIE_ROW_OVERFLOW : 0);
+        P.tk_key[r] = 0;
         P.cut_comp[r] = (p < 1.0f && cut != ~0ull) ? cut : 0;
         P.kept_mass[r] = T;
         P.row_mass[r] = sall;
@@ -1004,46 +812,282 @@ FIE_DEV void finalize_wide(const Params& P, int r, FinWideLds& L)
         L.scal[1] = chosen;
     }
     __syncthreads();
+    // logprobs of a wide row: the top-L candidates gathered for the rank list
+    if (P.logprobs[r] >= 0) {
+        const unsigned int na = ld_shared(&st.nA);
+        const int nA = na > (unsigned int)kCap ? kCap : (int)na;
+        if (P.logprobs[r] > 0) load_sorted(P.candA + (int64_t)r * kCap, nA, s, key);
+        write_logprobs(P, r, key, nA, M, sall, key_to_float((uint32_t)(L.scal[1] >> 32)));
+        if (tid == 0 && na > (unsigned int)kCap) set_status(P, r, FIE_ROW_OVERFLOW);
+    }
 }
 
-template <int DT>
-__global__ __launch_bounds__(kThreads) void k_pass3(Params P)
+// Restores the row's accumulators and histograms to zero for the next call.
+FIE_DEV void reset_row(const Params& P, int r, bool wide)
 {
-    __shared__ Pass3Lds L;
-    __shared__ int s_flag;
-    const int r = blockIdx.x / P.S, s = blockIdx.x % P.S;
     RowState& st = P.st[r];
-    if (!(st.mode3 & kM3CollectB)) return;
-    const PatchView pv = stage_patches(P, r, s, L.patch);
-    const uint32_t lo0 = st.wlo[0], hi0 = st.whi[0];
-    const uint32_t lo1 = st.nwin > 1 ? st.wlo[1] : 1u, hi1 = st.nwin > 1 ? st.whi[1] : 0u;
-    const float sc = P.scale[r], M = st.M, mp = P.min_p[r];
-    uint64_t* candB = P.candB + (int64_t)r * kCap;
-    for_each_element<DT>(P, r, s, pv, L.patch, [&](float w, uint32_t idx) {
-        const uint32_t k = fkey(w + 0.0f);
-        bool in = (k >= lo0 && k <= hi0) || (k >= lo1 && k <= hi1);
-        if (in && mp > 0.0f) in = !(cexp(scaled(w, sc) - M) < mp);
-        append_candidate(in, w, idx, &st.nB, candB);
-    });
-    if (!last_to_arrive(st, 2, P.S, &s_flag)) return;
-    finalize_wide(P, r, L.fin);
-    const uint64_t chosen = L.fin.scal[1];
-    const uint64_t sall = st.sall;
-    const int nA = (int)(st.nA_kept > (unsigned)kCap ? kCap : st.nA_kept);
-    const bool lpover = st.nA_kept > (unsigned)kCap;
-    __syncthreads();
-    // logprobs of wide rows: the top-L candidates gathered in pass 2
-    if (P.logprobs[r] >= 0) {
-        if (P.logprobs[r] > 0) load_sorted(P.candA + (int64_t)r * kCap, nA, sc, L.lp.key);
-        write_logprobs(P, r, L.lp.key, nA, M, sall, key_to_float((uint32_t)(chosen >> 32)));
+    if (wide) {
+        unsigned long long* gm = P.mmass + (int64_t)r * kMassBins;
+        uint32_t* gc = P.mcnt + (int64_t)r * kMassBins;
+        for (int b = threadIdx.x; b < kMassBins; b += kThreads) {
+            if (ld_shared(&gc[b])) {
+                st_shared(&gc[b], 0u);
+                st_shared(&gm[b], 0ull);
+            }
+        }
     }
     if (threadIdx.x == 0) {
-        if (lpover) P.status[r] |= FIE_ROW_OVERFLOW;
-        st.sall = 0;
-        st.nB = 0;
-        st.nA_kept = 0;
-        st.mode3 = 0;
+        st_shared(&st.maxpack, 0ull);
+        st_shared(&st.minkey_inv, 0u);
+        st_shared(&st.sall, 0ull);
+        st_shared(&st.nA, 0u);
+        st_shared(&st.nB, 0u);
+        st_shared(&st.overflow, 0u);
+        st_shared(&st.arrive[0], 0u);
+        st_shared(&st.arrive[1], 0u);
+        st_shared(&st.arrive[2], 0u);
     }
+}
+
+// ============================================================== the sampler step
+// One workgroup per (row, slice).  The slice (CPT 16-byte chunks per thread) is
+// read from HBM once into registers; every later phase works on the registers.
+template <int DT, int CPT>
+__global__ __launch_bounds__(kThreads) void k_sample(Params P)
+{
+    __shared__ SampleLds L;
+    constexpr int EPC = Dt<DT>::EPC;
+    constexpr int NE = CPT * EPC;
+    const int r = blockIdx.x / P.S, s = blockIdx.x % P.S;
+    const int tid = threadIdx.x;
+    RowState& st = P.st[r];
+    const bool argmax_only = P.argmax_only != 0;
+    const bool greedy = argmax_only || (P.flags[r] & 1);
+    const int Lp = argmax_only ? -1 : P.logprobs[r];
+    const int k = greedy ? 0 : P.top_k[r];
+    const int kind = greedy ? kKindGreedy : (k > 0 ? kKindTopK : kKindWide);
+    const int kk = kind == kKindTopK ? (k > Lp ? k : Lp) : Lp;
+    const bool need_sel = kk > 0;
+    const bool need_mass = kind == kKindWide || Lp >= 0;
+    const float sc = argmax_only ? 1.0f : P.scale[r];
+
+    // ---- the slice, into registers (penalty patches applied on the way)
+    PatchView pv{0, true, slice_begin(P, s), nullptr, nullptr};
+    if (!argmax_only) pv = stage_patches(P, r, s, L.patch);
+    const char* row = row_ptr(P, r);
+    const int64_t nch = (P.vocab + EPC - 1) / EPC;
+    const int64_t cbase = (int64_t)s * P.cps + tid;
+    float v[NE];
+    int nv[CPT];                         // valid elements in each chunk
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int64_t c = cbase + (int64_t)j * kThreads;
+        const int64_t left = (int64_t)P.vocab - c * EPC;
+        nv[j] = left >= EPC ? EPC : (left > 0 ? (int)left : 0);
+        if (nv[j] == EPC) {
+            load_chunk<DT>(row, c * EPC, P.vec_ok, &v[j * EPC]);
+        } else {
+#pragma unroll
+            for (int q = 0; q < EPC; ++q)
+                v[j * EPC + q] = (q < nv[j]) ? load_one<DT>(row, c * EPC + q) : -INFINITY;
+        }
+    }
+    if (pv.n) {
+#pragma unroll
+        for (int j = 0; j < CPT; ++j)
+            if (nv[j] > 0) apply_patches<EPC>(pv, L.patch, (cbase + (int64_t)j * kThreads) * EPC, &v[j * EPC]);
+    }
+    (void)nch;
+
+    // ---- phase 1: max (first index on ties), min, per-thread max
+    uint64_t best = 0;
+    uint32_t minv = 0;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const uint32_t e0 = (uint32_t)((cbase + (int64_t)j * kThreads) * EPC);
+#pragma unroll
+        for (int q = 0; q < EPC; ++q) {
+            if (q < nv[j]) {
+                const uint32_t key = fkey(v[j * EPC + q] + 0.0f);
+                const uint64_t pack = ((uint64_t)key << 32) | (0xFFFFFFFFu - (e0 + q));
+                best = pack > best ? pack : best;
+                minv = (~key) > minv ? ~key : minv;
+            }
+        }
+    }
+    const uint32_t tmax = (uint32_t)(best >> 32);
+    const uint64_t bbest = block_max_u64<kThreads>(best, L.red);
+    const uint64_t bmin = (kind == kKindWide) ? block_max_u64<kThreads>(minv, L.red) : 0;
+    if (tid == 0) {
+        atomicMax(&st.maxpack, (unsigned long long)bbest);
+        if (kind == kKindWide) atomicMax(&st.minkey_inv, (unsigned int)bmin);
+    }
+
+    if (kind == kKindGreedy && Lp < 0) {
+        // sampler.py:103-106 and :236-238: the argmax is the answer
+        if (arrive(&st.arrive[0], P.S, &L.flag) && tid == 0) {
+            const unsigned long long mp = ld_shared(&st.maxpack);
+            const int argmax = (int)(0xFFFFFFFFu - (uint32_t)(mp & 0xFFFFFFFFu));
+            P.tokens[r] = argmax;
+            if (!argmax_only) {
+                write_row_outputs_default(P, r);
+                P.row_max[r] = key_to_float((uint32_t)(mp >> 32));
+                P.kept_mass[r] = weight_of(1.0f);
+            }
+            st_shared(&st.maxpack, 0ull);
+            st_shared(&st.arrive[0], 0u);
+        }
+        return;
+    }
+
+    // ---- phase 2 (rank selection): histogram of keys that can be in the top kk.
+    // The kk-th largest per-thread maximum bounds the row's kk-th largest value
+    // from below, so smaller keys need not be counted.
+    if (need_sel) {
+        uint32_t theta = 0;
+        if (kk <= kThreads) {
+            // largest theta with #(thread maxima >= theta) >= kk, built bit by bit
+            // from the top (the count is non-increasing in theta): 32 fixed steps
+            for (int bit = 31; bit >= 0; --bit) {
+                const uint32_t cand = theta | (1u << bit);
+                const uint64_t m = __ballot(tmax >= cand);
+                if ((tid & 63) == 0) L.ured[tid >> 6] = (uint32_t)__popcll(m);
+                __syncthreads();
+                uint32_t cnt = 0;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) cnt += L.ured[w];
+                __syncthreads();
+                if (cnt >= (uint32_t)kk) theta = cand;
+            }
+        }
+        for (int i = tid; i < kCountBins; i += kThreads) L.u.chist[i] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < CPT; ++j)
+#pragma unroll
+            for (int q = 0; q < EPC; ++q)
+                if (q < nv[j]) {
+                    const uint32_t key = fkey(v[j * EPC + q] + 0.0f);
+                    if (key >= theta) atomicAdd(&L.u.chist[key >> kCountShift], 1u);
+                }
+        __syncthreads();
+        uint32_t* gh = P.chist + (int64_t)r * kCountBins;
+        for (int i = tid; i < kCountBins; i += kThreads)
+            if (L.u.chist[i]) atomicAdd(&gh[i], L.u.chist[i]);
+    }
+
+    // ---- hand-off 1: row max (and rank bin) for every workgroup of the row
+    if (arrive(&st.arrive[0], P.S, &L.flag)) {
+        uint32_t keyA = 0;
+        if (need_sel) keyA = plan_rank(P, r, kk, L);
+        if (tid == 0) {
+            const unsigned long long mp = ld_shared(&st.maxpack);
+            const float M = scaled(key_to_float((uint32_t)(mp >> 32)), sc);
+            st_shared(&st.M, M);
+            st_shared(&st.keyA, keyA);
+            if (kind == kKindWide) {
+                const float ymin = scaled(key_to_float(~ld_shared(&st.minkey_inv)), sc);
+                const float R = fminf(M - ymin, 28.0f);
+                st_shared(&st.dscale, (R > 0.0f) ? (float)(kMassBins - 1) / R : 0.0f);
+            }
+            P.row_max[r] = M;
+        }
+        publish_plan(&st.arrive[0]);
+    } else if (!wait_plan(&st.arrive[0], &L.flag)) {
+        if (tid == 0) set_status(P, r, FIE_ROW_TIMEOUT);
+        return;
+    }
+    const float M = ld_shared(&st.M);
+
+    // ---- phase 3: integer weights (row mass; survivor mass histogram of wide rows)
+    if (need_mass) {
+        const float ds = ld_shared(&st.dscale);
+        const float mp = P.min_p[r];
+        const bool hist = kind == kKindWide;
+        if (hist) {
+            for (int i = tid; i < kMassBins; i += kThreads) { L.u.mh.cnt[i] = 0; L.u.mh.mass[i] = 0; }
+            __syncthreads();
+        }
+        uint64_t sall = 0;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j)
+#pragma unroll
+            for (int q = 0; q < EPC; ++q)
+                if (q < nv[j]) {
+                    const float d = scaled(v[j * EPC + q], sc) - M;
+                    const float e = cexp(d);
+                    const uint64_t wt = weight_of(e);
+                    sall += wt;
+                    if (hist && !(mp > 0.0f && e < mp)) {
+                        const int b = d_bin(d, ds);
+                        atomicAdd(&L.u.mh.cnt[b], 1u);
+                        atomicAdd(&L.u.mh.mass[b], (unsigned long long)wt);
+                    }
+                }
+        sall = block_sum_u64<kThreads>(sall, L.red);
+        if (tid == 0) atomicAdd(&st.sall, (unsigned long long)sall);
+        if (hist) {
+            __syncthreads();
+            uint32_t* gc = P.mcnt + (int64_t)r * kMassBins;
+            unsigned long long* gm = P.mmass + (int64_t)r * kMassBins;
+            for (int i = tid; i < kMassBins; i += kThreads)
+                if (L.u.mh.cnt[i]) {
+                    atomicAdd(&gc[i], L.u.mh.cnt[i]);
+                    atomicAdd(&gm[i], L.u.mh.mass[i]);
+                }
+        }
+    }
+
+    // ---- hand-off 2 (wide rows): cut and draw windows
+    if (kind == kKindWide) {
+        if (arrive(&st.arrive[1], P.S, &L.flag)) {
+            plan_wide(P, r, L);
+            publish_plan(&st.arrive[1]);
+        } else if (!wait_plan(&st.arrive[1], &L.flag)) {
+            if (tid == 0) set_status(P, r, FIE_ROW_TIMEOUT);
+            return;
+        }
+        const uint32_t lo0 = ld_shared(&st.wlo[0]), hi0 = ld_shared(&st.whi[0]);
+        const int nw = ld_shared(&st.nwin);
+        const uint32_t lo1 = nw > 1 ? ld_shared(&st.wlo[1]) : 1u;
+        const uint32_t hi1 = nw > 1 ? ld_shared(&st.whi[1]) : 0u;
+        const float mp = P.min_p[r];
+        uint64_t* candB = P.candB + (int64_t)r * kCap;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const uint32_t e0 = (uint32_t)((cbase + (int64_t)j * kThreads) * EPC);
+#pragma unroll
+            for (int q = 0; q < EPC; ++q) {
+                const float w = v[j * EPC + q];
+                const uint32_t key = fkey(w + 0.0f);
+                bool in = q < nv[j] && ((key >= lo0 && key <= hi0) || (key >= lo1 && key <= hi1));
+                if (in && mp > 0.0f) in = !(cexp(scaled(w, sc) - M) < mp);
+                append_candidate(in, w, e0 + q, &st.nB, candB);
+            }
+        }
+    }
+
+    // ---- rank candidates (top-k survivors, logprob lists)
+    if (need_sel) {
+        const uint32_t keyA = ld_shared(&st.keyA);
+        uint64_t* candA = P.candA + (int64_t)r * kCap;
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const uint32_t e0 = (uint32_t)((cbase + (int64_t)j * kThreads) * EPC);
+#pragma unroll
+            for (int q = 0; q < EPC; ++q) {
+                const float w = v[j * EPC + q];
+                append_candidate(q < nv[j] && fkey(w + 0.0f) >= keyA, w, e0 + q, &st.nA, candA);
+            }
+        }
+    }
+
+    // ---- the last workgroup finishes the row
+    if (!arrive(&st.arrive[2], P.S, &L.flag)) return;
+    if (kind == kKindWide) finalize_wide(P, r, L);
+    else finalize_topk(P, r, kind, L);
+    __syncthreads();
+    reset_row(P, r, kind == kKindWide);
 }
 
 // ============================================================== kept set / probs
@@ -1249,18 +1293,15 @@ static int check_launch(const char* what)
     return FIE_OK;
 }
 
-static int slices_for(int rows, int vocab, int epc)
+// Chunks per slice: 256 threads x CPT 16-byte chunks, CPT = 8 unless that leaves
+// fewer than 1024 workgroups (small batches), then CPT = 2.
+static void choose_slices(Params& P)
 {
-    const int nch = (vocab + epc - 1) / epc;
-    int S = (2048 + rows - 1) / (rows > 0 ? rows : 1);
-    const int smax_small = vocab / kMinSlice > 0 ? vocab / kMinSlice : 1;
-    if (S > smax_small) S = smax_small;
-    const int smin = (vocab + kMaxSlice - 65) / (kMaxSlice - 64);
-    if (S < smin) S = smin;
-    if (S > kMaxSlices) S = kMaxSlices;
-    if (S > nch) S = nch;
-    if (S < 1) S = 1;
-    return S;
+    const int64_t nch = (P.vocab + P.epc - 1) / P.epc;
+    int cpt = 8;
+    if ((int64_t)P.rows * ((nch + kThreads * 8 - 1) / (kThreads * 8)) < 1024) cpt = 2;
+    P.cps = kThreads * cpt;
+    P.S = (int)((nch + P.cps - 1) / P.cps);
 }
 
 static int fill_layout(Params& P, const fie_workspace* ws, int rows, int64_t hist)
@@ -1309,10 +1350,8 @@ static int fill_params(Params& P, const fie_sampler_args* a, const fie_workspace
     P.lp_cols = a->lp_cols;
     P.epc = 16 / es;
     P.vec_ok = (((uintptr_t)a->logits % 16) == 0 && (P.row_stride_bytes % 16) == 0) ? 1 : 0;
-    P.S = slices_for(a->rows, a->vocab, P.epc);
-    const int nch = (a->vocab + P.epc - 1) / P.epc;
-    P.cps = (nch + P.S - 1) / P.S;
-    P.S = (nch + P.cps - 1) / P.cps;
+    choose_slices(P);
+    if (P.S > kMaxSlices) return fail(FIE_E_ARG, "vocab too large for the slice table");
     P.apply_pen = a->apply_penalties ? 1 : 0;
     P.epoch = a->epoch;
     P.scale = a->scale; P.top_k = a->top_k; P.top_p = a->top_p; P.min_p = a->min_p;
@@ -1331,6 +1370,32 @@ static int fill_params(Params& P, const fie_sampler_args* a, const fie_workspace
     if (P.apply_pen && (!P.rep || !P.pres || !P.freq || !P.hist_off || (a->hist_total > 0 && !P.hist_ids)))
         return fail(FIE_E_ARG, "penalty arrays are NULL");
     return fill_layout(P, ws, a->rows, P.apply_pen ? a->hist_total : 0);
+}
+
+template <int DT>
+static void launch_sample(const Params& P, hipStream_t st)
+{
+    const dim3 grid((unsigned)(P.rows * P.S)), block(kThreads);
+    if (P.cps == kThreads * 8) hipLaunchKernelGGL((k_sample<DT, 8>), grid, block, 0, st, P);
+    else hipLaunchKernelGGL((k_sample<DT, 2>), grid, block, 0, st, P);
+}
+
+static int launch_stage(const Params& P, int stage, hipStream_t st)
+{
+    switch (stage) {
+    case FIE_STAGE_PENALTY:
+        if (!P.apply_pen) return FIE_OK;
+        hipLaunchKernelGGL(k_penalty, dim3(P.rows), dim3(kPenThreads),
+                           (size_t)((P.vocab + 31) / 32) * 2 * sizeof(uint32_t), st, P);
+        return check_launch("k_penalty");
+    case FIE_STAGE_SAMPLE:
+        if (P.dtype == FIE_F32) launch_sample<FIE_F32>(P, st);
+        else if (P.dtype == FIE_F16) launch_sample<FIE_F16>(P, st);
+        else launch_sample<FIE_BF16>(P, st);
+        return check_launch("k_sample");
+    default:
+        return fail(FIE_E_ARG, "unknown stage");
+    }
 }
 
 extern "C" {
@@ -1356,26 +1421,18 @@ int fie_sampler_sample(const fie_sampler_args* a, const fie_workspace* ws, void*
     Params P;
     int rc = fill_params(P, a, ws);
     if (rc) return rc;
-    hipStream_t st = (hipStream_t)stream;
-    const dim3 grid((unsigned)(P.rows * P.S)), block(kThreads);
-    if (P.apply_pen) {
-        const int words = (P.vocab + 31) / 32;
-        hipLaunchKernelGGL(k_penalty, dim3(P.rows), dim3(kPenThreads),
-                           (size_t)words * 2 * sizeof(uint32_t), st, P);
-        if ((rc = check_launch("k_penalty"))) return rc;
-    }
-    if (P.dtype == FIE_F32) hipLaunchKernelGGL(k_pass1<FIE_F32>, grid, block, 0, st, P);
-    else if (P.dtype == FIE_F16) hipLaunchKernelGGL(k_pass1<FIE_F16>, grid, block, 0, st, P);
-    else hipLaunchKernelGGL(k_pass1<FIE_BF16>, grid, block, 0, st, P);
-    if ((rc = check_launch("k_pass1"))) return rc;
-    if (P.dtype == FIE_F32) hipLaunchKernelGGL(k_pass2<FIE_F32>, grid, block, 0, st, P);
-    else if (P.dtype == FIE_F16) hipLaunchKernelGGL(k_pass2<FIE_F16>, grid, block, 0, st, P);
-    else hipLaunchKernelGGL(k_pass2<FIE_BF16>, grid, block, 0, st, P);
-    if ((rc = check_launch("k_pass2"))) return rc;
-    if (P.dtype == FIE_F32) hipLaunchKernelGGL(k_pass3<FIE_F32>, grid, block, 0, st, P);
-    else if (P.dtype == FIE_F16) hipLaunchKernelGGL(k_pass3<FIE_F16>, grid, block, 0, st, P);
-    else hipLaunchKernelGGL(k_pass3<FIE_BF16>, grid, block, 0, st, P);
-    return check_launch("k_pass3");
+    for (int stage = FIE_STAGE_PENALTY; stage <= FIE_STAGE_SAMPLE; ++stage)
+        if ((rc = launch_stage(P, stage, (hipStream_t)stream))) return rc;
+    return FIE_OK;
+}
+
+int fie_sampler_stage(const fie_sampler_args* a, const fie_workspace* ws, int32_t stage,
+                      void* stream)
+{
+    Params P;
+    int rc = fill_params(P, a, ws);
+    if (rc) return rc;
+    return launch_stage(P, stage, (hipStream_t)stream);
 }
 
 int fie_sampler_resolve_overflow(const fie_sampler_args* a, const int32_t* row_list,
@@ -1421,20 +1478,13 @@ int fie_sampler_argmax(const void* logits, int32_t dtype, int32_t rows, int32_t 
     P.vocab = vocab;
     P.epc = 16 / es;
     P.vec_ok = (((uintptr_t)logits % 16) == 0 && (P.row_stride_bytes % 16) == 0) ? 1 : 0;
-    P.S = slices_for(rows, vocab, P.epc);
-    const int nch = (vocab + P.epc - 1) / P.epc;
-    P.cps = (nch + P.S - 1) / P.S;
-    P.S = (nch + P.cps - 1) / P.cps;
+    choose_slices(P);
+    if (P.S > kMaxSlices) return fail(FIE_E_ARG, "vocab too large for the slice table");
     P.argmax_only = 1;
     P.tokens = tokens;
     int rc = fill_layout(P, ws, rows, 0);
     if (rc) return rc;
-    hipStream_t st = (hipStream_t)stream;
-    const dim3 grid((unsigned)(rows * P.S)), block(kThreads);
-    if (dtype == FIE_F32) hipLaunchKernelGGL(k_pass1<FIE_F32>, grid, block, 0, st, P);
-    else if (dtype == FIE_F16) hipLaunchKernelGGL(k_pass1<FIE_F16>, grid, block, 0, st, P);
-    else hipLaunchKernelGGL(k_pass1<FIE_BF16>, grid, block, 0, st, P);
-    return check_launch("k_pass1(argmax)");
+    return launch_stage(P, FIE_STAGE_SAMPLE, (hipStream_t)stream);
 }
 
 int fie_sampler_kept(const fie_sampler_args* a, uint8_t* kept, float* probs,

@@ -15,6 +15,8 @@ LIB_PATH = os.path.join(_HERE, "_native", "libfie_sampler.so")
 FIE_OK = 0
 FIE_F32, FIE_F16, FIE_BF16 = 0, 1, 2
 FIE_ROW_OVERFLOW = 1
+FIE_ROW_TIMEOUT = 2
+FIE_STAGE_PENALTY, FIE_STAGE_SAMPLE = 0, 1
 LP_COLS = 20
 
 _vp = ctypes.c_void_p
@@ -47,6 +49,7 @@ class Workspace(ctypes.Structure):
 
 EXPORTS = (
     "fie_sampler_workspace_size", "fie_sampler_workspace_init", "fie_sampler_sample",
+    "fie_sampler_stage",
     "fie_sampler_resolve_overflow", "fie_sampler_argmax", "fie_sampler_kept",
     "fie_sampler_cexp", "fie_sampler_last_error",
 )
@@ -73,6 +76,8 @@ def load():
     lib.fie_sampler_workspace_size.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int64]
     lib.fie_sampler_workspace_init.argtypes = [ctypes.POINTER(Workspace), _vp]
     lib.fie_sampler_sample.argtypes = [ctypes.POINTER(SamplerArgs), ctypes.POINTER(Workspace), _vp]
+    lib.fie_sampler_stage.argtypes = [
+        ctypes.POINTER(SamplerArgs), ctypes.POINTER(Workspace), ctypes.c_int32, _vp]
     lib.fie_sampler_resolve_overflow.argtypes = [
         ctypes.POINTER(SamplerArgs), _vp, ctypes.c_int32, ctypes.POINTER(Workspace), _vp]
     lib.fie_sampler_argmax.argtypes = [

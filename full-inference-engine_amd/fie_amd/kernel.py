@@ -25,9 +25,10 @@ PARAM_FIELDS = (
     ("flags", np.int32), ("logprobs", np.int32), ("uniform", np.float64),
     ("rep", np.float32), ("pres", np.float32), ("freq", np.float32),
 )
-# Per-row outputs in download order (unsigned keys travel as same-width signed).
+# Per-row outputs in download order.  `status` is uploaded too (as zeros: the
+# kernels OR bits into it) and sits first so one copy each way covers it.
 OUTPUT_FIELDS = (
-    ("tokens", np.int64, 1), ("status", np.int32, 1), ("tk_key", np.uint32, 1),
+    ("status", np.int32, 1), ("tokens", np.int64, 1), ("tk_key", np.uint32, 1),
     ("cut_comp", np.uint64, 1), ("row_max", np.float32, 1), ("kept_mass", np.uint64, 1),
     ("row_mass", np.uint64, 1), ("chosen_lp", np.float32, 1),
     ("top_ids", np.int64, LP_COLS), ("top_lp", np.float32, LP_COLS),
@@ -78,11 +79,11 @@ class DeviceStep:
         o = _align(o + (rows + 1) * 8)
         offs["hist_ids"] = o
         o = _align(o + max(hist_total, 1) * 4)
-        self.param_bytes = o
+        self.out_begin = o
         for name, dt, width in OUTPUT_FIELDS:
             offs[name] = o
             o = _align(o + rows * width * np.dtype(dt).itemsize)
-        self.out_begin = self.param_bytes
+        self.param_bytes = offs[OUTPUT_FIELDS[1][0]]      # params + zeroed status
         self.total = o
         self.offs = offs
         self.dev = torch.empty(self.total, dtype=torch.uint8, device=device)
@@ -109,6 +110,7 @@ class DeviceStep:
         n = int(hp.hist_off[-1])
         if n:
             self.host_view("hist_ids", np.int32, n)[:] = hp.hist_ids
+        self.host_view("status", np.int32, self.rows)[:] = 0
 
     def upload(self, stream: torch.cuda.Stream) -> None:
         with torch.cuda.stream(stream):
@@ -218,6 +220,12 @@ class FusedSampler:
             self.reset_workspace()
         _lib.check(rc, "fie_sampler_sample")
 
+    def launch_stage(self, args: SamplerArgs, hist_total: int, stage: int) -> None:
+        ws = self.ensure_workspace(args.rows, args.vocab, hist_total)
+        rc = self.lib.fie_sampler_stage(ctypes.byref(args), ctypes.byref(ws), stage,
+                                        self._stream_ptr())
+        _lib.check(rc, f"fie_sampler_stage({stage})")
+
     def resolve_overflow(self, args: SamplerArgs, rows: list[int], hist_total: int) -> None:
         ws = self.ensure_workspace(args.rows, args.vocab, hist_total)
         lst = torch.tensor(rows, dtype=torch.int32, device=self.device)
@@ -270,8 +278,10 @@ class FusedSampler:
         buf.download(stream)
         stream.synchronize()
         out = buf.outputs()
-        over = np.nonzero(out["status"] & _lib.FIE_ROW_OVERFLOW)[0]
+        over = np.nonzero(out["status"])[0]
         if over.size:
+            if (out["status"] & _lib.FIE_ROW_TIMEOUT).any():
+                self.reset_workspace()
             self.resolve_overflow(args, [int(r) for r in over], hist_total)
             buf.download(stream)
             stream.synchronize()

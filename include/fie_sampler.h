@@ -40,11 +40,14 @@ enum {
 
 enum { FIE_F32 = 0, FIE_F16 = 1, FIE_BF16 = 2 };
 
-/* Per-row status bits written to fie_sampler_args.status. */
+/* Per-row status bits, OR-ed into fie_sampler_args.status (zero it before a call).
+   Either bit means the row's outputs are not final: pass the row to
+   fie_sampler_resolve_overflow.  After FIE_ROW_TIMEOUT also re-initialise the
+   workspace before its next use. */
 enum {
     FIE_ROW_OK = 0,
-    FIE_ROW_OVERFLOW = 1,  /* candidate set exceeded the fast path; row needs the exact
-                              fallback (fie_sampler_resolve_overflow) */
+    FIE_ROW_OVERFLOW = 1,  /* candidate set exceeded the fast path's capacity */
+    FIE_ROW_TIMEOUT = 2,   /* a bounded wait between the row's workgroups gave up */
 };
 
 typedef struct fie_sampler_args {
@@ -81,7 +84,7 @@ typedef struct fie_sampler_args {
 
     /* Outputs. */
     int64_t* tokens;            /* [rows] chosen token ids */
-    int32_t* status;            /* [rows] FIE_ROW_* bits */
+    int32_t* status;            /* [rows] FIE_ROW_* bits, zeroed by the caller */
     uint32_t* tk_key;           /* [rows] order key of the top-k threshold value (0 = none) */
     uint64_t* cut_comp;         /* [rows] (key<<32 | ~index) of the last top-p survivor (0 = none) */
     float* row_max;             /* [rows] largest scaled logit M */
@@ -111,6 +114,17 @@ int fie_sampler_workspace_init(const fie_workspace* ws, void* stream);
 
 /* One sampler step: sampler.py:81-117 minus host bookkeeping. */
 int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, void* stream);
+
+/* The kernels of fie_sampler_sample, one at a time, in this order (same args and
+   workspace each time).  No counterpart in the reference: it exists so a profiler
+   or a benchmark can time each kernel of the chain separately. */
+enum {
+    FIE_STAGE_PENALTY = 0,     /* history counts and penalised values; skipped when
+                                  apply_penalties == 0 */
+    FIE_STAGE_SAMPLE = 1,      /* the fused step: one read of the logits */
+};
+int fie_sampler_stage(const fie_sampler_args* args, const fie_workspace* ws, int32_t stage,
+                      void* stream);
 
 /* Exact fallback for rows whose status has FIE_ROW_OVERFLOW after
    fie_sampler_sample (same args and workspace, before any other call on it).
