@@ -99,6 +99,7 @@ struct Params {
     int64_t row_stride_bytes;
     int32_t dtype, rows, vocab, lp_cols;
     int32_t S;              // slices per row
+    int32_t groups;         // row groups of the persistent launch
     int32_t cps;            // chunks per slice
     int32_t epc;            // elements per 16-byte chunk
     int32_t vec_ok;         // rows are 16-byte aligned

@@ -400,6 +400,16 @@ __global__ __launch_bounds__(kPenThreads) void k_penalty(Params P)
     }
 }
 
+// ============================================================== diagnostics
+// Optional per-(row, slice) phase timestamps (wall clock, 100 MHz) for profiling.
+__device__ uint64_t* g_trace = nullptr;
+
+FIE_DEV void trace_mark(int r, int s, int S, int i)
+{
+    uint64_t* t = g_trace;
+    if (t != nullptr && threadIdx.x == 0) t[((int64_t)r * S + s) * 8 + i] = wall_clock64();
+}
+
 // ============================================================== row hand-off
 // The workgroups of one row cooperate through three arrival counters in the
 // row's state.  A workgroup publishes its partial results (agent-scope atomics),
@@ -850,15 +860,13 @@ FIE_DEV void reset_row(const Params& P, int r, bool wide)
 }
 
 // ============================================================== the sampler step
-// One workgroup per (row, slice).  The slice (CPT 16-byte chunks per thread) is
-// read from HBM once into registers; every later phase works on the registers.
+// Slice s of row r.  The slice (CPT 16-byte chunks per thread) is read from HBM
+// once into registers; every later phase works on the registers.
 template <int DT, int CPT>
-__global__ __launch_bounds__(kThreads) void k_sample(Params P)
+FIE_DEV void sample_row(const Params& P, int r, int s, SampleLds& L)
 {
-    __shared__ SampleLds L;
     constexpr int EPC = Dt<DT>::EPC;
     constexpr int NE = CPT * EPC;
-    const int r = blockIdx.x / P.S, s = blockIdx.x % P.S;
     const int tid = threadIdx.x;
     RowState& st = P.st[r];
     const bool argmax_only = P.argmax_only != 0;
@@ -870,6 +878,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(Params P)
     const bool need_sel = kk > 0;
     const bool need_mass = kind == kKindWide || Lp >= 0;
     const float sc = argmax_only ? 1.0f : P.scale[r];
+    trace_mark(r, s, P.S, 0);
 
     // ---- the slice, into registers (penalty patches applied on the way)
     PatchView pv{0, true, slice_begin(P, s), nullptr, nullptr};
@@ -898,6 +907,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(Params P)
             if (nv[j] > 0) apply_patches<EPC>(pv, L.patch, (cbase + (int64_t)j * kThreads) * EPC, &v[j * EPC]);
     }
     (void)nch;
+    trace_mark(r, s, P.S, 1);
 
     // ---- phase 1: max (first index on ties), min, per-thread max
     uint64_t best = 0;
@@ -977,6 +987,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(Params P)
     }
 
     // ---- hand-off 1: row max (and rank bin) for every workgroup of the row
+    trace_mark(r, s, P.S, 2);
     if (arrive(&st.arrive[0], P.S, &L.flag)) {
         uint32_t keyA = 0;
         if (need_sel) keyA = plan_rank(P, r, kk, L);
@@ -998,6 +1009,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(Params P)
         return;
     }
     const float M = ld_shared(&st.M);
+    trace_mark(r, s, P.S, 3);
 
     // ---- phase 3: integer weights (row mass; survivor mass histogram of wide rows)
     if (need_mass) {
@@ -1039,6 +1051,7 @@ __global__ __launch_bounds__(kThreads) void k_sample(Params P)
     }
 
     // ---- hand-off 2 (wide rows): cut and draw windows
+    trace_mark(r, s, P.S, 4);
     if (kind == kKindWide) {
         if (arrive(&st.arrive[1], P.S, &L.flag)) {
             plan_wide(P, r, L);
@@ -1083,11 +1096,29 @@ __global__ __launch_bounds__(kThreads) void k_sample(Params P)
     }
 
     // ---- the last workgroup finishes the row
-    if (!arrive(&st.arrive[2], P.S, &L.flag)) return;
+    trace_mark(r, s, P.S, 5);
+    if (!arrive(&st.arrive[2], P.S, &L.flag)) { trace_mark(r, s, P.S, 6); return; }
+    trace_mark(r, s, P.S, 6);
     if (kind == kKindWide) finalize_wide(P, r, L);
     else finalize_topk(P, r, kind, L);
     __syncthreads();
     reset_row(P, r, kind == kKindWide);
+    trace_mark(r, s, P.S, 7);
+}
+
+// Persistent row groups: the grid is as large as the GPU holds at once, in
+// groups of S consecutive workgroups; group g handles rows g, g + groups, ...,
+// so the S workgroups that cooperate on a row start it together and every wait
+// is on a workgroup that is already running.
+template <int DT, int CPT>
+__global__ __launch_bounds__(kThreads) void k_sample(Params P)
+{
+    __shared__ SampleLds L;
+    const int g = blockIdx.x / P.S, s = blockIdx.x % P.S;
+    for (int r = g; r < P.rows; r += P.groups) {
+        sample_row<DT, CPT>(P, r, s, L);
+        __syncthreads();
+    }
 }
 
 // ============================================================== kept set / probs
@@ -1372,12 +1403,35 @@ static int fill_params(Params& P, const fie_sampler_args* a, const fie_workspace
     return fill_layout(P, ws, a->rows, P.apply_pen ? a->hist_total : 0);
 }
 
+// Workgroups of a kernel that the device holds at once.
+static int resident_capacity(const void* kernel)
+{
+    int dev = 0, cus = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, kThreads, 0) != hipSuccess) return 0;
+    return cus * per;
+}
+
+template <int DT, int CPT>
+static void launch_sample_cpt(Params P, hipStream_t st)
+{
+    const void* fn = (const void*)k_sample<DT, CPT>;
+    static thread_local int cap = -1;
+    if (cap < 0) cap = resident_capacity(fn);
+    int groups = cap / P.S;
+    if (groups < 1) groups = 1;
+    if (groups > P.rows) groups = P.rows;
+    P.groups = groups;
+    hipLaunchKernelGGL((k_sample<DT, CPT>), dim3((unsigned)(groups * P.S)), dim3(kThreads), 0,
+                       st, P);
+}
+
 template <int DT>
 static void launch_sample(const Params& P, hipStream_t st)
 {
-    const dim3 grid((unsigned)(P.rows * P.S)), block(kThreads);
-    if (P.cps == kThreads * 8) hipLaunchKernelGGL((k_sample<DT, 8>), grid, block, 0, st, P);
-    else hipLaunchKernelGGL((k_sample<DT, 2>), grid, block, 0, st, P);
+    if (P.cps == kThreads * 8) launch_sample_cpt<DT, 8>(P, st);
+    else launch_sample_cpt<DT, 2>(P, st);
 }
 
 static int launch_stage(const Params& P, int stage, hipStream_t st)
@@ -1510,5 +1564,13 @@ int fie_sampler_cexp(const float* in, float* out, int64_t n, void* stream)
 }
 
 const char* fie_sampler_last_error(void) { return g_err; }
+
+int fie_sampler_set_trace(void* buffer)
+{
+    uint64_t* p = (uint64_t*)buffer;
+    if (hipMemcpyToSymbol(HIP_SYMBOL(g_trace), &p, sizeof p) != hipSuccess)
+        return fail(FIE_E_LAUNCH, "cannot set the trace buffer");
+    return FIE_OK;
+}
 
 }  // extern "C"

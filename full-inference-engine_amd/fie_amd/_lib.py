@@ -51,7 +51,7 @@ EXPORTS = (
     "fie_sampler_workspace_size", "fie_sampler_workspace_init", "fie_sampler_sample",
     "fie_sampler_stage",
     "fie_sampler_resolve_overflow", "fie_sampler_argmax", "fie_sampler_kept",
-    "fie_sampler_cexp", "fie_sampler_last_error",
+    "fie_sampler_cexp", "fie_sampler_last_error", "fie_sampler_set_trace",
 )
 
 _lib = None
@@ -86,6 +86,7 @@ def load():
     lib.fie_sampler_kept.argtypes = [
         ctypes.POINTER(SamplerArgs), _vp, _vp, ctypes.POINTER(Workspace), _vp]
     lib.fie_sampler_cexp.argtypes = [_vp, _vp, ctypes.c_int64, _vp]
+    lib.fie_sampler_set_trace.argtypes = [_vp]
     lib.fie_sampler_last_error.restype = ctypes.c_char_p
     for name in EXPORTS:
         if name not in ("fie_sampler_workspace_size", "fie_sampler_last_error"):

@@ -147,6 +147,12 @@ int fie_sampler_kept(const fie_sampler_args* args, uint8_t* kept, float* probs,
 /* The build's canonical fp32 exponential on n device values (verification aid). */
 int fie_sampler_cexp(const float* in, float* out, int64_t n, void* stream);
 
+/* Profiling aid, no counterpart in the reference: when `buffer` (device memory,
+   rows * slices * 8 uint64) is not NULL, every later fie_sampler_sample records
+   wall-clock timestamps at the phase boundaries of each (row, slice) workgroup.
+   NULL switches it off. */
+int fie_sampler_set_trace(void* buffer);
+
 /* Message of the last failing call on this thread (static storage). */
 const char* fie_sampler_last_error(void);
 
