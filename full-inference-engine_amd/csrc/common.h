@@ -1,5 +1,6 @@
-// Shared device helpers of the MI355X sampler: order keys, the canonical
-// exponential, fixed-point weights, exact integer scaling, block scans.
+// Device helpers of the MI355X sampler: order keys, the canonical exponential,
+// fixed-point weights, exact 128/192-bit integer scaling, wave64 and block
+// reductions.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -9,16 +10,21 @@
 
 namespace fie {
 
-constexpr int kThreads = 256;                 // pass kernels: 4 wave64 per workgroup
-constexpr int kWaves = kThreads / 64;
+typedef unsigned __int128 u128;
+
+// Tokens per tile.  Part of the canonical weight rule: a token's weight is taken
+// relative to the largest scaled logit of its tile (token 0 is a tile of its own,
+// then [1, kTile), [kTile, 2 kTile), ...).
+constexpr int kTile = 8192;
 
 // ---------------------------------------------------------------- order keys
-// Order-preserving key of an fp32 value (larger value -> larger key).  Callers
-// fold -0 into +0 first so equal values have equal keys.
+// Order-preserving key of an fp32 value: larger value -> larger key.  Callers fold
+// -0 into +0 first (v + 0.0f) so equal values have equal keys.  Keys of non-NaN
+// values are never 0, which the kernels use as "no element".
 FIE_DEV uint32_t fkey(float v)
 {
     uint32_t b = __float_as_uint(v);
-    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return b ^ ((uint32_t)((int32_t)b >> 31) | 0x80000000u);
 }
 
 FIE_DEV float key_to_float(uint32_t k)
@@ -30,22 +36,23 @@ FIE_DEV float key_to_float(uint32_t k)
 constexpr uint32_t kKeyNegInf = 0x007FFFFFu;  // fkey(-inf)
 constexpr uint32_t kKeyPosInf = 0xFF800000u;  // fkey(+inf)
 
-// Rank order of the sampler: value descending, then token index ascending.
-FIE_DEV uint64_t comp_key(uint32_t ykey, uint32_t idx)
+// Rank order of the sampler: value descending, then token index ascending, as one
+// u64 compared descending.
+FIE_DEV uint64_t comp_key(uint32_t key, uint32_t idx)
 {
-    return ((uint64_t)ykey << 32) | (uint64_t)(0xFFFFFFFFu - idx);
+    return ((uint64_t)key << 32) | (uint64_t)(0xFFFFFFFFu - idx);
 }
+FIE_DEV uint32_t comp_idx(uint64_t c) { return 0xFFFFFFFFu - (uint32_t)c; }
+FIE_DEV uint32_t comp_k(uint64_t c) { return (uint32_t)(c >> 32); }
 
-FIE_DEV uint32_t comp_idx(uint64_t c) { return 0xFFFFFFFFu - (uint32_t)(c & 0xFFFFFFFFu); }
-
-// The scaled logit y = w / s exactly as sampler.py:185 computes it (IEEE divide),
-// with -0 folded into +0.
+// The scaled logit exactly as sampler.py:185 computes it (IEEE fp32 divide), with
+// -0 folded into +0.
 FIE_DEV float scaled(float w, float s) { return w / s + 0.0f; }
 
 // ---------------------------------------------------------------- exponential
 // Canonical fp32 exponential of d <= 0: Cody-Waite reduction by a two-part ln 2,
 // degree-7 Taylor polynomial on |r| <= ln2/2 by Horner with fused multiply-adds,
-// exact scaling by 2^n.  Every step is one IEEE binary32 operation, so any
+// exact scaling by 2^n.  Each step is one IEEE binary32 operation, so any
 // implementation performing the same steps returns the same bits.
 FIE_DEV float cexp(float d)
 {
@@ -65,69 +72,72 @@ FIE_DEV float cexp(float d)
     return __builtin_ldexpf(p, (int)n);
 }
 
-// floor(e * 2^40) of e in [0, 1]: the integer weight of a token.  e * 2^40 is an
-// exact product, so the conversion only truncates.
-FIE_DEV uint64_t weight_of(float e)
+// floor(e * 2^40) of e in [0, 1].  e * 2^40 is exact in double, so the conversion
+// only truncates.
+FIE_DEV uint64_t fixed40(float e)
 {
     return (uint64_t)((double)e * 1099511627776.0);
 }
 
-// ceil(p * S) for an fp32 p in (0, 1) and S < 2^63, exactly.
-FIE_DEV uint64_t ceil_mul_f32(float p, uint64_t S)
+// Token weight relative to its tile maximum m: floor(cexp(y - m) * 2^40).
+FIE_DEV uint64_t tok_weight(float y, float m) { return fixed40(cexp(y - m)); }
+
+// ---------------------------------------------------------------- wide integers
+FIE_DEV u128 mul64(uint64_t a, uint64_t b) { return (u128)a * b; }
+
+// floor(m * X / 2^q) for m < 2^53, X < 2^128, exactly (a 192-bit product).
+FIE_DEV u128 mul_shift(uint64_t m, u128 X, int q)
+{
+    u128 lo = (u128)m * (uint64_t)X;
+    u128 hi = (u128)m * (uint64_t)(X >> 64);
+    uint64_t p0 = (uint64_t)lo;
+    u128 mid = (lo >> 64) + hi;
+    uint64_t p1 = (uint64_t)mid;
+    uint64_t p2 = (uint64_t)(mid >> 64);
+    if (q >= 192) return 0;
+    if (q >= 128) return (u128)(p2 >> (q - 128));
+    if (q >= 64) {
+        int s = q - 64;
+        u128 v = ((u128)p2 << 64) | p1;
+        return s ? (v >> s) : v;
+    }
+    u128 v = ((u128)p1 << 64) | p0;
+    return q ? ((v >> q) | ((u128)p2 << (128 - q))) : v;
+}
+
+// Exact ceil(p * S) for an fp32 p in (0, 1) and S < 2^104.
+FIE_DEV u128 ceil_mul_f32(float p, u128 S)
 {
     uint32_t b = __float_as_uint(p);
     uint32_t eb = (b >> 23) & 0xFFu;
     uint64_t mant = (b & 0x7FFFFFu) | (eb ? 0x800000u : 0u);
     int q = eb ? 150 - (int)eb : 149;
-    unsigned __int128 prod = (unsigned __int128)mant * S;
-    if (q >= 127) return prod ? 1 : 0;
-    unsigned __int128 fl = prod >> q;
-    return (uint64_t)(fl + (((fl << q) != prod) ? 1 : 0));
+    u128 P = (u128)mant * S;
+    if (q >= 128) return P ? 1 : 0;
+    return (P >> q) + (((P & ((((u128)1) << q) - 1)) != 0) ? 1 : 0);
 }
 
-// floor(u * T) for a double u in [0, 1) and T < 2^63, exactly.
-FIE_DEV uint64_t floor_mul_f64(double u, uint64_t T)
+// Exact floor(u * K) for a double u in [0, 1) and K < 2^104.
+FIE_DEV u128 floor_mul_f64(double u, u128 K)
 {
     if (!(u > 0.0)) return 0;
     uint64_t b = (uint64_t)__double_as_longlong(u);
     uint32_t eb = (uint32_t)((b >> 52) & 0x7FFu);
     uint64_t mant = (b & 0xFFFFFFFFFFFFFull) | (eb ? (1ull << 52) : 0ull);
     int q = eb ? 1075 - (int)eb : 1074;
-    if (q >= 127) return 0;
-    unsigned __int128 prod = (unsigned __int128)mant * T;
-    return (uint64_t)(prod >> q);
+    return mul_shift(mant, K, q);
 }
 
-// ---------------------------------------------------------------- coherence
-// Workgroups of one pass hand results to the row's last workgroup without an
-// agent-scope fence (which writes back and invalidates the whole L2 of an XCD):
-// every value crossing workgroups is an agent-scope atomic (RMW, or a load/store
-// with the sc1 coherence bit), and a writer drains its memory counters before it
-// signals arrival, which orders those accesses the way the release fence would.
-template <typename T>
-FIE_DEV T ld_shared(const T* p)
+FIE_DEV double u128_to_double(u128 x)
 {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return (double)(uint64_t)(x >> 64) * 18446744073709551616.0 + (double)(uint64_t)x;
 }
 
-template <typename T>
-FIE_DEV void st_shared(T* p, T v)
+// ---------------------------------------------------------------- wave64 helpers
+FIE_DEV uint64_t shfl_xor_u64(uint64_t v, int m)
 {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-FIE_DEV void drain_memory()
-{
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    __builtin_amdgcn_s_waitcnt(0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-// ---------------------------------------------------------------- reductions
-FIE_DEV uint64_t shfl_u64(uint64_t v, int src)
-{
-    uint32_t lo = __shfl((uint32_t)v, src, 64);
-    uint32_t hi = __shfl((uint32_t)(v >> 32), src, 64);
+    uint32_t lo = __shfl_xor((uint32_t)v, m, 64);
+    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
     return ((uint64_t)hi << 32) | lo;
 }
 
@@ -138,35 +148,23 @@ FIE_DEV uint64_t shfl_up_u64(uint64_t v, int d)
     return ((uint64_t)hi << 32) | lo;
 }
 
-FIE_DEV uint64_t shfl_xor_u64(uint64_t v, int m)
+FIE_DEV uint64_t shfl_u64(uint64_t v, int src)
 {
-    uint32_t lo = __shfl_xor((uint32_t)v, m, 64);
-    uint32_t hi = __shfl_xor((uint32_t)(v >> 32), m, 64);
+    uint32_t lo = __shfl((uint32_t)v, src, 64);
+    uint32_t hi = __shfl((uint32_t)(v >> 32), src, 64);
     return ((uint64_t)hi << 32) | lo;
 }
 
-FIE_DEV uint64_t wave_max_u64(uint64_t v)
+FIE_DEV u128 shfl_up_u128(u128 v, int d)
 {
-    for (int m = 32; m > 0; m >>= 1) {
-        uint64_t o = shfl_xor_u64(v, m);
-        v = o > v ? o : v;
-    }
-    return v;
+    uint64_t lo = shfl_up_u64((uint64_t)v, d), hi = shfl_up_u64((uint64_t)(v >> 64), d);
+    return ((u128)hi << 64) | lo;
 }
 
-FIE_DEV uint64_t wave_min_u64(uint64_t v)
+FIE_DEV u128 shfl_xor_u128(u128 v, int m)
 {
-    for (int m = 32; m > 0; m >>= 1) {
-        uint64_t o = shfl_xor_u64(v, m);
-        v = o < v ? o : v;
-    }
-    return v;
-}
-
-FIE_DEV uint64_t wave_sum_u64(uint64_t v)
-{
-    for (int m = 32; m > 0; m >>= 1) v += shfl_xor_u64(v, m);
-    return v;
+    uint64_t lo = shfl_xor_u64((uint64_t)v, m), hi = shfl_xor_u64((uint64_t)(v >> 64), m);
+    return ((u128)hi << 64) | lo;
 }
 
 FIE_DEV uint32_t wave_max_u32(uint32_t v)
@@ -178,50 +176,97 @@ FIE_DEV uint32_t wave_max_u32(uint32_t v)
     return v;
 }
 
-// Inclusive scan over the 64 lanes of a wave.
-FIE_DEV uint64_t wave_incl_scan_u64(uint64_t v)
+FIE_DEV uint32_t wave_min_u32(uint32_t v)
+{
+    for (int m = 32; m > 0; m >>= 1) {
+        uint32_t o = __shfl_xor(v, m, 64);
+        v = o < v ? o : v;
+    }
+    return v;
+}
+
+FIE_DEV uint32_t wave_sum_u32(uint32_t v)
+{
+    for (int m = 32; m > 0; m >>= 1) v += __shfl_xor(v, m, 64);
+    return v;
+}
+
+FIE_DEV uint64_t wave_max_u64(uint64_t v)
+{
+    for (int m = 32; m > 0; m >>= 1) {
+        uint64_t o = shfl_xor_u64(v, m);
+        v = o > v ? o : v;
+    }
+    return v;
+}
+
+FIE_DEV uint64_t wave_sum_u64(uint64_t v)
+{
+    for (int m = 32; m > 0; m >>= 1) v += shfl_xor_u64(v, m);
+    return v;
+}
+
+FIE_DEV u128 wave_sum_u128(u128 v)
+{
+    for (int m = 32; m > 0; m >>= 1) v += shfl_xor_u128(v, m);
+    return v;
+}
+
+// Inclusive prefix sum over the lanes of a wave (lane 0 first).
+FIE_DEV uint32_t wave_incl_scan_u32(uint32_t v)
 {
     const int lane = threadIdx.x & 63;
     for (int d = 1; d < 64; d <<= 1) {
-        uint64_t o = shfl_up_u64(v, d);
+        uint32_t o = __shfl_up(v, d, 64);
         if (lane >= d) v += o;
     }
     return v;
 }
 
-// Block-wide exclusive scan of one u64 per thread (blockDim.x == nthreads, a
-// multiple of 64, at most 1024).  `scratch` holds nthreads/64 + 1 values.
-template <int NT>
-FIE_DEV uint64_t block_excl_scan_u64(uint64_t v, uint64_t* scratch, uint64_t* total)
+FIE_DEV u128 wave_incl_scan_u128(u128 v)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    uint64_t incl = wave_incl_scan_u64(v);
-    if (lane == 63) scratch[wave] = incl;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        uint64_t run = 0;
-        for (int w = 0; w < NT / 64; ++w) {
-            uint64_t t = scratch[w];
-            scratch[w] = run;
-            run += t;
-        }
-        scratch[NT / 64] = run;
+    const int lane = threadIdx.x & 63;
+    for (int d = 1; d < 64; d <<= 1) {
+        u128 o = shfl_up_u128(v, d);
+        if (lane >= d) v += o;
     }
+    return v;
+}
+
+// ---------------------------------------------------------------- block helpers
+// All take a __shared__ scratch area of at least NT/64 entries of the value type
+// and end with a barrier, so the scratch can be reused at once.
+template <int NT>
+FIE_DEV uint32_t block_max_u32(uint32_t v, uint32_t* scratch)
+{
+    v = wave_max_u32(v);
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
     __syncthreads();
-    uint64_t res = scratch[wave] + incl - v;
-    *total = scratch[NT / 64];
+    uint32_t t = 0;
+    for (int w = 0; w < NT / 64; ++w) t = scratch[w] > t ? scratch[w] : t;
     __syncthreads();
-    return res;
+    return t;
 }
 
 template <int NT>
-FIE_DEV uint64_t block_sum_u64(uint64_t v, uint64_t* scratch)
+FIE_DEV uint32_t block_min_u32(uint32_t v, uint32_t* scratch)
 {
-    v = wave_sum_u64(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) scratch[wave] = v;
+    v = wave_min_u32(v);
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
     __syncthreads();
-    uint64_t t = 0;
+    uint32_t t = 0xFFFFFFFFu;
+    for (int w = 0; w < NT / 64; ++w) t = scratch[w] < t ? scratch[w] : t;
+    __syncthreads();
+    return t;
+}
+
+template <int NT>
+FIE_DEV uint32_t block_sum_u32(uint32_t v, uint32_t* scratch)
+{
+    v = wave_sum_u32(v);
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+    __syncthreads();
+    uint32_t t = 0;
     for (int w = 0; w < NT / 64; ++w) t += scratch[w];
     __syncthreads();
     return t;
@@ -231,8 +276,7 @@ template <int NT>
 FIE_DEV uint64_t block_max_u64(uint64_t v, uint64_t* scratch)
 {
     v = wave_max_u64(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) scratch[wave] = v;
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
     __syncthreads();
     uint64_t t = 0;
     for (int w = 0; w < NT / 64; ++w) t = scratch[w] > t ? scratch[w] : t;
@@ -241,45 +285,45 @@ FIE_DEV uint64_t block_max_u64(uint64_t v, uint64_t* scratch)
 }
 
 template <int NT>
-FIE_DEV uint64_t block_min_u64(uint64_t v, uint64_t* scratch)
+FIE_DEV uint64_t block_sum_u64(uint64_t v, uint64_t* scratch)
 {
-    v = wave_min_u64(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (lane == 0) scratch[wave] = v;
+    v = wave_sum_u64(v);
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
     __syncthreads();
-    uint64_t t = ~0ull;
-    for (int w = 0; w < NT / 64; ++w) t = scratch[w] < t ? scratch[w] : t;
+    uint64_t t = 0;
+    for (int w = 0; w < NT / 64; ++w) t += scratch[w];
     __syncthreads();
     return t;
 }
 
-// In-LDS bitonic sort of n (a power of two) u64 keys into descending order.
 template <int NT>
-FIE_DEV void bitonic_sort_desc(uint64_t* key, int n)
+FIE_DEV u128 block_sum_u128(u128 v, u128* scratch)
 {
-    for (int k = 2; k <= n; k <<= 1) {
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            for (int i = threadIdx.x; i < n; i += NT) {
-                int ixj = i ^ j;
-                if (ixj > i) {
-                    uint64_t a = key[i], b = key[ixj];
-                    bool up = (i & k) != 0;            // this pair ends ascending
-                    if (up ? (a > b) : (a < b)) {
-                        key[i] = b;
-                        key[ixj] = a;
-                    }
-                }
-            }
-            __syncthreads();
-        }
-    }
+    v = wave_sum_u128(v);
+    if ((threadIdx.x & 63) == 0) scratch[threadIdx.x >> 6] = v;
+    __syncthreads();
+    u128 t = 0;
+    for (int w = 0; w < NT / 64; ++w) t += scratch[w];
+    __syncthreads();
+    return t;
 }
 
-FIE_DEV int pow2_at_least(int n)
+// Exclusive prefix sum in thread order; *total receives the block sum.
+template <int NT>
+FIE_DEV uint32_t block_excl_scan_u32(uint32_t v, uint32_t* scratch, uint32_t* total)
 {
-    int p = 64;
-    while (p < n) p <<= 1;
-    return p;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t incl = wave_incl_scan_u32(v);
+    if (lane == 63) scratch[wave] = incl;
+    __syncthreads();
+    uint32_t before = 0, all = 0;
+    for (int w = 0; w < NT / 64; ++w) {
+        if (w < wave) before += scratch[w];
+        all += scratch[w];
+    }
+    __syncthreads();
+    *total = all;
+    return before + incl - v;
 }
 
 }  // namespace fie

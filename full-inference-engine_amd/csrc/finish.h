@@ -1,0 +1,698 @@
+// The per-row kernel of the sampler (k_finish): one workgroup of 512 threads per row.
+//
+// It merges the tile partials of k_scan (maxima, masses, top tokens), settles token
+// 0's penalty, and decides the row exactly on the candidate set whenever the
+// decision provably lies among the candidates: every token whose scaled key is
+// above the largest tile bound was streamed out, so a threshold, a cut or a draw
+// that lands above that key is final.  Otherwise the row takes the full-row path
+// in the same workgroup: radix passes that re-read the row from memory, narrowing a
+// key range until it fits in LDS, then the same LDS selection.
+#pragma once
+
+#include "scan.h"
+
+namespace fie {
+
+constexpr int kFinThreads = 512;
+constexpr int kGCap = 8192;        // composites held in LDS (candidates / a gathered bin)
+constexpr int kPassBins = 2048;    // bins of a full-row radix pass
+
+// Radix digits over the 64-bit rank composite (key << 32 | ~index): three over the
+// key, then three over the index (bits 31..24 of ~index are constant for V < 2^24).
+struct Digit {
+    int shift, bits;
+};
+__device__ constexpr Digit kDigits[6] = {{53, 11}, {42, 11}, {32, 10}, {21, 11}, {10, 11}, {0, 10}};
+
+struct SelResult {
+    uint64_t comp;       // the element where the running measure crosses the target
+    u128 excl;           // measure of the selected set ranked before it
+    u128 meas;           // its own measure
+    int found;
+};
+
+struct FinSmem {
+    uint64_t cand[kGCap];                       // candidates or a gathered key range
+    uint32_t pc[kPassBins];                     // full-row pass: counts per bin
+    uint64_t pm_lo[kPassBins], pm_hi[kPassBins];// full-row pass: mass per bin
+    uint32_t cnt[kTile];                        // penalty counts of one tile
+    uint32_t hc[256];                           // LDS selection: counts per digit
+    uint64_t hm_lo[256], hm_hi[256];            // LDS selection: mass per digit
+    float mt[kMaxTiles + 1];                    // tile maxima of y (slot 0 = token 0)
+    uint64_t ct[kMaxTiles + 1];                 // tile scales C_t
+    uint64_t tmc[kMaxTiles];                    // tile maxima composites (x keys)
+    uint32_t coff[kMaxTiles + 1];               // candidate offsets per tile
+    uint64_t red64[16];
+    u128 red128[16];
+    uint32_t red32[32];
+    uint32_t n, zc, bad;
+    int ibin, flag;
+    uint64_t bcomp[2];
+    u128 bex, bme;
+    uint32_t bcnt;
+    SelResult sel;
+};
+
+// Weight of a y-domain composite under rule R1: floor(cexp(y - m_t) 2^40) * C_t.
+FIE_DEV u128 comp_weight(const FinSmem& S, uint64_t c)
+{
+    const uint32_t idx = comp_idx(c);
+    const int slot = idx == 0 ? 0 : 1 + (int)(idx / kTile);
+    const float y = key_to_float(comp_k(c));
+    return (u128)tok_weight(y, S.mt[slot]) * S.ct[slot];
+}
+
+// Predicate shared by every selection: the element survives top-k / min-p (key >=
+// tau), lies above the safety key (key > safe), and is kept by the top-p cut
+// (composite >= cut, cut = 0 for none).
+struct Pred {
+    uint32_t tau;
+    uint32_t safe;   // 0 = no restriction (keys are never 0)
+    uint64_t cut;
+    FIE_DEV bool operator()(uint64_t c) const
+    {
+        const uint32_t k = comp_k(c);
+        return k >= tau && k > safe && c >= cut;
+    }
+};
+
+// ---------------------------------------------------------------- LDS selection
+// Radix selection over S.cand[0, n): among elements satisfying `pr`, in descending
+// composite order, the element where the running measure (count, or weight when
+// MASS) first exceeds g: excl <= g < excl + meas.  Digits are 8-bit windows placed
+// just below the common prefix of the remaining range, so few levels are needed.
+template <bool MASS>
+FIE_DEV SelResult lds_select(FinSmem& S, int n, const Pred pr, u128 g)
+{
+    const int tid = threadIdx.x;
+    uint64_t prefix = 0, pmask = 0;
+    u128 excl = 0;
+    for (int level = 0; level < 64; ++level) {
+        // range of the remaining elements
+        uint64_t mn = ~0ull, mx = 0;
+        for (int i = tid; i < n; i += kFinThreads) {
+            const uint64_t c = S.cand[i];
+            if ((c & pmask) == prefix && pr(c)) {
+                mn = c < mn ? c : mn;
+                mx = c > mx ? c : mx;
+            }
+        }
+        mx = block_max_u64<kFinThreads>(mx, S.red64);
+        mn = ~block_max_u64<kFinThreads>(~mn, S.red64);
+        if (mx == 0 && mn == ~0ull) return SelResult{0, 0, 0, 0};
+        if (mn == mx) {
+            const u128 m = MASS ? comp_weight(S, mx) : (u128)1;
+            return SelResult{mx, excl, m, g < m ? 1 : 0};
+        }
+        const int hb = 63 - __builtin_clzll(mn ^ mx);
+        const int shift = hb >= 7 ? hb - 7 : 0;
+        for (int i = tid; i < 256; i += kFinThreads) {
+            S.hc[i] = 0;
+            if (MASS) { S.hm_lo[i] = 0; S.hm_hi[i] = 0; }
+        }
+        __syncthreads();
+        const uint64_t hmask = (hb >= 63) ? 0ull : ~((2ull << hb) - 1);
+        for (int i = tid; i < n; i += kFinThreads) {
+            const uint64_t c = S.cand[i];
+            if ((c & hmask) == (mn & hmask) && (c & pmask) == prefix && pr(c)) {
+                const int d = (int)((c >> shift) & 0xFFu);
+                atomicAdd(&S.hc[d], 1u);
+                if (MASS) {
+                    const u128 w = comp_weight(S, c);
+                    const uint64_t lo = (uint64_t)w;
+                    const uint64_t old = atomicAdd((unsigned long long*)&S.hm_lo[d], (unsigned long long)lo);
+                    const uint64_t carry = (old + lo < old) ? 1ull : 0ull;
+                    const uint64_t hi = (uint64_t)(w >> 64) + carry;
+                    if (hi) atomicAdd((unsigned long long*)&S.hm_hi[d], (unsigned long long)hi);
+                }
+            }
+        }
+        __syncthreads();
+        // wave 0 scans the 256 digits from the top
+        if (tid < 64) {
+            u128 loc[4];
+            u128 sum = 0;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const int d = 255 - (tid * 4 + q);
+                loc[q] = MASS ? (((u128)S.hm_hi[d] << 64) | S.hm_lo[d]) : (u128)S.hc[d];
+                sum += loc[q];
+            }
+            const u128 incl = wave_incl_scan_u128(sum);
+            u128 run = incl - sum;
+            if (run <= g && g < incl) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    if (run <= g && g < run + loc[q]) {
+                        S.ibin = 255 - (tid * 4 + q);
+                        S.bex = run;
+                    }
+                    run += loc[q];
+                }
+            }
+            if (tid == 63 && !(g < incl)) { S.ibin = -1; S.bex = incl; }
+        }
+        __syncthreads();
+        const int d = S.ibin;
+        const u128 above = S.bex;
+        __syncthreads();
+        if (d < 0) return SelResult{0, excl + above, 0, 0};
+        g -= above;
+        excl += above;
+        prefix = (mn & hmask) | ((uint64_t)d << shift);
+        pmask = ~((1ull << shift) - 1) | hmask;
+        if (shift == 0) pmask = ~0ull;
+    }
+    return SelResult{0, 0, 0, 0};
+}
+
+// ---------------------------------------------------------------- full-row passes
+// Penalty counts of tile [lo, hi) of `row` into S.cnt (one u32 per token).
+FIE_DEV void recount(FinSmem& S, const fie_sampler_args& a, int row, int lo, int hi)
+{
+    for (int i = threadIdx.x; i < kTile; i += kFinThreads) S.cnt[i] = 0;
+    __syncthreads();
+    const int64_t h0 = a.hist_offsets[row], h1 = a.hist_offsets[row + 1];
+    for (int64_t h = h0 + threadIdx.x; h < h1; h += kFinThreads) {
+        const uint32_t id = (uint32_t)a.hist_ids[h];
+        if (id >= (uint32_t)lo && id < (uint32_t)hi && id != 0) {
+            atomicAdd(&S.cnt[id - lo], 1u);
+        }
+    }
+    __syncthreads();
+}
+
+// Visit every token of the row once, re-reading it from memory: f(comp) with the
+// y-domain composite of each token (token 0 with its settled value y0).
+template <int DT, bool VEC, class F>
+FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, float rep,
+                      float pres, float freq, uint32_t k0, F&& f)
+{
+    constexpr int EPL = DTy<DT>::EPL, SZ = DTy<DT>::SZ;
+    constexpr int NL = kTile / kFinThreads / EPL;
+    const fie_sampler_args& a = P.a;
+    const int V = a.vocab, tid = threadIdx.x;
+    const char* rowp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * SZ;
+    if (tid == 0 && k0) f(comp_key(k0, 0));
+    for (int tile = 0; tile < P.NT; ++tile) {
+        const int lo = tile * kTile, hi = min(lo + kTile, V);
+        uint4 raw[NL];
+#pragma unroll
+        for (int j = 0; j < NL; ++j) raw[j] = load_group<DT, VEC>(rowp, lo + (j * kFinThreads + tid) * EPL, V);
+        if (pen) recount(S, a, row, lo, hi);
+#pragma unroll
+        for (int j = 0; j < NL; ++j) {
+            const int e0 = lo + (j * kFinThreads + tid) * EPL;
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) {
+                const int idx = e0 + e;
+                if (idx >= V || idx == 0) continue;
+                float x = lane_get<DT>(raw[j], e);
+                if (pen) {
+                    const uint32_t cc = S.cnt[idx - lo];
+                    if (cc) x = penalize(x, rep, pres, freq, cc);
+                }
+                const float y = s == 1.0f ? x + 0.0f : scaled(x, s);
+                f(comp_key(fkey(y), (uint32_t)idx));
+            }
+        }
+        if (pen) __syncthreads();
+    }
+    __syncthreads();
+}
+
+// Count (and mass) histogram of one digit level over the elements satisfying pr
+// whose composite bits above the digit equal `hiprefix`.
+template <int DT, bool VEC, bool MASS>
+FIE_DEV void pass_hist(FinSmem& S, const KParams& P, int row, float s, bool pen, float rep,
+                       float pres, float freq, uint32_t k0, const Pred pr, int level,
+                       uint64_t hiprefix)
+{
+    const Digit dg = kDigits[level];
+    const int top = dg.shift + dg.bits;
+    const uint32_t dmask = (1u << dg.bits) - 1;
+    for (int i = threadIdx.x; i < kPassBins; i += kFinThreads) {
+        S.pc[i] = 0;
+        if (MASS) { S.pm_lo[i] = 0; S.pm_hi[i] = 0; }
+    }
+    __syncthreads();
+    row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](uint64_t c) {
+        if ((top >= 64 || (c >> top) == hiprefix) && pr(c)) {
+            const uint32_t d = (uint32_t)(c >> dg.shift) & dmask;
+            atomicAdd(&S.pc[d], 1u);
+            if (MASS) {
+                const u128 w = comp_weight(S, c);
+                const uint64_t lo = (uint64_t)w;
+                const uint64_t old = atomicAdd((unsigned long long*)&S.pm_lo[d], (unsigned long long)lo);
+                const uint64_t hi = (uint64_t)(w >> 64) + ((old + lo < old) ? 1ull : 0ull);
+                if (hi) atomicAdd((unsigned long long*)&S.pm_hi[d], (unsigned long long)hi);
+            }
+        }
+    });
+}
+
+// Descending scan of the pass histogram for the bin where the running measure
+// crosses g.  Returns the bin (-1 if the total is <= g) with S.bex = measure above
+// it and S.bcnt = its count.
+template <bool MASS>
+FIE_DEV int pass_pick(FinSmem& S, int nbins, u128 g)
+{
+    const int tid = threadIdx.x;
+    const int per = (nbins + kFinThreads - 1) / kFinThreads;   // 1..4
+    u128 sum = 0;
+    for (int q = 0; q < per; ++q) {
+        const int b = nbins - 1 - (tid * per + q);
+        if (b >= 0) sum += MASS ? (((u128)S.pm_hi[b] << 64) | S.pm_lo[b]) : (u128)S.pc[b];
+    }
+    // block exclusive scan of u128 in thread order
+    const int lane = tid & 63, wave = tid >> 6;
+    const u128 incl = wave_incl_scan_u128(sum);
+    if (lane == 63) S.red128[wave] = incl;
+    if (tid == 0) S.ibin = -1;
+    __syncthreads();
+    u128 before = 0, all = 0;
+    for (int w = 0; w < kFinThreads / 64; ++w) {
+        if (w < wave) before += S.red128[w];
+        all += S.red128[w];
+    }
+    before += incl - sum;
+    if (before <= g && g < before + sum) {
+        u128 run = before;
+        for (int q = 0; q < per; ++q) {
+            const int b = nbins - 1 - (tid * per + q);
+            if (b < 0) break;
+            const u128 m = MASS ? (((u128)S.pm_hi[b] << 64) | S.pm_lo[b]) : (u128)S.pc[b];
+            if (run <= g && g < run + m) {
+                S.ibin = b;
+                S.bex = run;
+                S.bcnt = S.pc[b];
+            }
+            run += m;
+        }
+    }
+    if (tid == 0 && !(g < all)) S.bex = all;
+    __syncthreads();
+    const int b = S.ibin;
+    __syncthreads();
+    return b;
+}
+
+// Gather the elements satisfying pr whose composite bits from `top` up equal
+// `hiprefix` into S.cand; returns their number (the caller ensures <= kGCap).
+template <int DT, bool VEC>
+FIE_DEV int pass_gather(FinSmem& S, const KParams& P, int row, float s, bool pen, float rep,
+                        float pres, float freq, uint32_t k0, const Pred pr, int top,
+                        uint64_t hiprefix)
+{
+    if (threadIdx.x == 0) S.n = 0;
+    __syncthreads();
+    row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](uint64_t c) {
+        if ((top >= 64 || (c >> top) == hiprefix) && pr(c)) {
+            const uint32_t at = atomicAdd(&S.n, 1u);
+            if (at < (uint32_t)kGCap) S.cand[at] = c;
+        }
+    });
+    const int n = (int)S.n;
+    __syncthreads();
+    return n;
+}
+
+// Full-row selection: radix levels over re-read passes until the selected key
+// range fits in LDS, then the LDS selection.  When `have_l1` the level-0 pass
+// histogram for the same predicate is already in S (and `l1_adjust` has been
+// applied by the caller).
+template <int DT, bool VEC, bool MASS>
+FIE_DEV SelResult row_select(FinSmem& S, const KParams& P, int row, float s, bool pen, float rep,
+                             float pres, float freq, uint32_t k0, const Pred pr, u128 g,
+                             bool have_l1)
+{
+    uint64_t hiprefix = 0;
+    u128 excl = 0;
+    for (int level = 0; level < 6; ++level) {
+        const Digit dg = kDigits[level];
+        if (!(level == 0 && have_l1))
+            pass_hist<DT, VEC, MASS>(S, P, row, s, pen, rep, pres, freq, k0, pr, level, hiprefix);
+        const int b = pass_pick<MASS>(S, 1 << dg.bits, g);
+        if (b < 0) return SelResult{0, excl + S.bex, 0, 0};
+        const u128 above = S.bex;
+        const uint32_t cnt = S.bcnt;
+        __syncthreads();
+        g -= above;
+        excl += above;
+        hiprefix = (hiprefix << dg.bits) | (uint64_t)b;
+        if (cnt <= (uint32_t)kGCap) {
+            const int n = pass_gather<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, pr,
+                                               dg.shift, hiprefix);
+            SelResult r = lds_select<MASS>(S, n, pr, g);
+            r.excl += excl;
+            return r;
+        }
+    }
+    return SelResult{0, 0, 0, 0};
+}
+
+// Smallest y-key K with cexp(key_to_float(K) - M) >= mp (rule R5 as a threshold;
+// cexp is non-decreasing).  0 when mp <= 0.
+FIE_DEV uint32_t minp_key(float M, float mp)
+{
+    if (!(mp > 0.0f)) return 0;
+    uint32_t lo = kKeyNegInf, hi = fkey(M);
+    if (!(cexp(key_to_float(hi) - M) >= mp)) return hi;   // degenerate rows (M not finite)
+    while (hi - lo > 1) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (cexp(key_to_float(mid) - M) >= mp) hi = mid;
+        else lo = mid;
+    }
+    return hi;
+}
+
+// Token 0 keeps its penalty iff the row is the widest of the batch (no pad entry
+// rewrites index 0 after it) and no id >= vocab first occurs after it
+// (sampler.py:148,156-157,174-175 with a sequential scatter).
+FIE_DEV bool q1_keeps(FinSmem& S, const KParams& P, int row)
+{
+    const fie_sampler_args& a = P.a;
+    const int NT = P.NT, B = a.rows, tid = threadIdx.x;
+    auto nu_of = [&](int r) -> uint32_t {
+        if (!(a.flags[r] & FIE_FLAG_PENALTY)) return 0u;
+        uint32_t u = P.w.tok0c[r] ? 1u : 0u;
+        if (a.hist_invalid) u += (uint32_t)a.hist_invalid[r] & 0x3FFFFFFFu;
+        return u;
+    };
+    uint32_t mine = 0, wmax = 0;
+    for (int r = tid; r < B; r += kFinThreads) {
+        uint32_t u = nu_of(r);
+        for (int t = 0; t < NT; ++t) u += P.w.nu[(size_t)r * NT + t];
+        wmax = u > wmax ? u : wmax;
+        if (r == row) S.red32[31] = u;
+    }
+    wmax = block_max_u32<kFinThreads>(wmax, S.red32);
+    mine = S.red32[31];
+    __syncthreads();
+    const bool late = a.hist_invalid && (((uint32_t)a.hist_invalid[row] >> 30) & 1u);
+    return mine == wmax && !late;
+}
+
+// ---------------------------------------------------------------- k_finish
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
+{
+    __shared__ FinSmem S;
+    const fie_sampler_args& a = P.a;
+    const int row = blockIdx.x, tid = threadIdx.x, NT = P.NT;
+    const int32_t fl = a.flags[row];
+    const bool greedy = fl & FIE_FLAG_GREEDY;
+    const int lp = a.logprobs ? a.logprobs[row] : -1;
+    const bool pen = a.apply_penalties && (fl & FIE_FLAG_PENALTY);
+    const int topk = greedy ? 0 : a.top_k[row];
+    const float tp = greedy ? 1.0f : a.top_p[row];
+    const float mp = greedy ? 0.0f : a.min_p[row];
+    const float s = greedy ? 1.0f : a.scale[row];
+    const bool need_mass = lp >= 0 || (!greedy && topk == 0);
+    float rep = 1.0f, pres = 0.0f, freq = 0.0f;
+    if (pen) { rep = a.repetition[row]; pres = a.presence[row]; freq = a.frequency[row]; }
+    int32_t status = 0;
+    if (pen && P.w.bad[row] && !a.hist_invalid) status |= FIE_ROW_UNCOUNTED_IDS;
+
+    // Tile maxima (x keys) and the row maximum.
+    if (tid < NT) S.tmc[tid] = P.w.maxc[(size_t)row * NT + tid];
+    __syncthreads();
+    const uint64_t xm = block_max_u64<kFinThreads>(tid < NT ? S.tmc[tid] : 0ull, S.red64);
+
+    // Token 0 (a tile of its own).
+    const float x0 = P.w.tok0x[row];
+    const uint32_t c0 = pen ? P.w.tok0c[row] : 0u;
+    float w0 = x0;
+    if (c0 && q1_keeps(S, P, row)) w0 = penalize(x0, rep, pres, freq, c0);
+    const float y0 = s == 1.0f ? w0 + 0.0f : scaled(w0, s);
+    const uint32_t k0 = fkey(y0);
+
+    // Row maximum M of y and the tile table of rule R1.
+    const uint32_t kxm = xm ? fkey(y_of_xkey(comp_k(xm), s)) : 0u;
+    const uint32_t Mkey = kxm > k0 ? kxm : k0;
+    const float M = key_to_float(Mkey);
+    if (tid <= NT) {
+        float mt;
+        uint64_t ct;
+        if (tid == 0) {
+            mt = y0;
+            ct = fixed40(cexp(y0 - M));
+        } else {
+            const uint64_t c = S.tmc[tid - 1];
+            mt = c ? y_of_xkey(comp_k(c), s) : 0.0f;
+            ct = c ? fixed40(cexp(mt - M)) : 0ull;
+        }
+        S.mt[tid] = mt;
+        S.ct[tid] = ct;
+        P.w.mt[(size_t)row * (NT + 1) + tid] = mt;
+        P.w.ct[(size_t)row * (NT + 1) + tid] = ct;
+    }
+    __syncthreads();
+
+    // Whole-row mass (rule R1): sum over tiles of C_t * (tile sum of weights).
+    u128 sall = 0;
+    if (need_mass) {
+        u128 part = 0;
+        if (tid < NT) part = (u128)S.ct[tid + 1] * P.w.sw[(size_t)row * NT + tid];
+        if (tid == 0) part += (u128)tok_weight(y0, y0) * S.ct[0];
+        sall = block_sum_u128<kFinThreads>(part, S.red128);
+    }
+
+    int64_t token = -1;
+    uint64_t tok_comp = 0;   // y-domain composite of the chosen token
+    uint32_t tau = 0;
+    uint64_t cut = 0;
+    u128 T = 0;
+    bool deep = false;
+    double lse = 0.0;
+    if (lp >= 0) lse = log(u128_to_double(sall)) - 80.0 * 0.69314718055994530942;
+
+    // Greedy rows: argmax, first index on ties (sampler.py:106,236-238).
+    if (greedy) {
+        const uint64_t best = xm > comp_key(k0, 0) ? xm : comp_key(k0, 0);
+        token = comp_idx(best);
+        tok_comp = best;
+        T = comp_weight(S, best);
+    }
+
+    // Candidates as y-domain composites, and the safety key: every token whose
+    // scaled key exceeds `safe` is among them.
+    int n = 0;
+    uint32_t safe = 0;
+    const bool need_cand = !greedy || lp > 0;
+    if (need_cand) {
+        if (tid == 0) {
+            uint32_t off = 0, kx = 0;
+            for (int t = 0; t < NT; ++t) {
+                S.coff[t] = off;
+                off += P.w.ncand[(size_t)row * NT + t];
+                const uint32_t b = P.w.bound[(size_t)row * NT + t];
+                kx = b > kx ? b : kx;
+            }
+            S.coff[NT] = off;
+            S.n = off + 1;
+            S.red32[0] = kx;
+        }
+        __syncthreads();
+        n = (int)S.n;
+        const uint32_t kx = S.red32[0];
+        __syncthreads();
+        if (kx <= 1u || kx <= kKeyNegInf) safe = 0;
+        else if (kx > kKeyPosInf) safe = 0xFFFFFFFFu;
+        else safe = fkey(y_of_xkey(kx, s));
+        if (n > kGCap) {
+            deep = true;
+        } else {
+            for (int t = 0; t < NT; ++t) {
+                const uint32_t o = S.coff[t], m = S.coff[t + 1] - o;
+                const uint64_t* src = P.w.cand + ((size_t)row * NT + t) * kCap;
+                for (uint32_t i = tid; i < m; i += kFinThreads) {
+                    const uint64_t xc = src[i];
+                    S.cand[o + i] = comp_key(fkey(y_of_xkey(comp_k(xc), s)), comp_idx(xc));
+                }
+            }
+            if (tid == 0) S.cand[n - 1] = comp_key(k0, 0);
+            __syncthreads();
+        }
+    }
+
+    // Sampled rows on the candidates: top-k, min-p, S, top-p cut, draw.
+    if (!greedy && !deep) {
+        const Pred all{0, 0, 0};
+        uint32_t tk = 0;
+        if (topk > 0) {
+            if (n < topk) deep = true;
+            else {
+                const SelResult r = lds_select<false>(S, n, all, (u128)(topk - 1));
+                tk = comp_k(r.comp);
+                if (!r.found || tk <= safe) deep = true;
+            }
+        }
+        const uint32_t tmp = minp_key(M, mp);
+        tau = tk > tmp ? tk : tmp;
+        if (!deep && tau != 0 && tau <= safe) deep = true;
+        if (!deep) {
+            u128 Sv = sall;
+            if (tau != 0) {
+                u128 part = 0;
+                for (int i = tid; i < n; i += kFinThreads)
+                    if (comp_k(S.cand[i]) >= tau) part += comp_weight(S, S.cand[i]);
+                Sv = block_sum_u128<kFinThreads>(part, S.red128);
+            }
+            const Pred surv{tau, safe, 0};
+            if (tp < 1.0f) {
+                const u128 thr = ceil_mul_f32(tp, Sv);
+                const SelResult r = lds_select<true>(S, n, surv, thr - 1);
+                if (!r.found) deep = true;
+                else { cut = r.comp; T = r.excl + r.meas; }
+            } else {
+                T = Sv;
+            }
+            if (!deep) {
+                if (T == 0) {
+                    const SelResult r = lds_select<false>(S, n, all, 0);
+                    token = comp_idx(r.comp);
+                    tok_comp = r.comp;
+                } else {
+                    const u128 g = floor_mul_f64(a.uniform[row], T);
+                    const SelResult r = lds_select<true>(S, n, Pred{tau, safe, cut}, g);
+                    if (!r.found) deep = true;
+                    else { token = comp_idx(r.comp); tok_comp = r.comp; }
+                }
+            }
+        }
+        if (!deep && a.tk_key && tid == 0) a.tk_key[row] = tk;
+    }
+
+    // Full-row path for sampled rows the candidates could not settle.
+    if (!greedy && deep) {
+        status |= FIE_ROW_EXACT_PATH;
+        cut = 0;
+        uint32_t tk = 0;
+        if (topk > 0) {
+            const SelResult r = row_select<DT, VEC, false>(S, P, row, s, pen, rep, pres, freq, k0,
+                                                           Pred{0, 0, 0}, (u128)(topk - 1), false);
+            tk = comp_k(r.comp);
+        }
+        const uint32_t tmp = minp_key(M, mp);
+        tau = tk > tmp ? tk : tmp;
+        const Pred surv{tau, 0, 0};
+        pass_hist<DT, VEC, true>(S, P, row, s, pen, rep, pres, freq, k0, surv, 0, 0);
+        u128 part = 0;
+        for (int b = tid; b < kPassBins; b += kFinThreads)
+            part += ((u128)S.pm_hi[b] << 64) | S.pm_lo[b];
+        const u128 Sv = block_sum_u128<kFinThreads>(part, S.red128);
+        bool l1 = true;
+        if (tp < 1.0f) {
+            const u128 thr = ceil_mul_f32(tp, Sv);
+            const SelResult r = row_select<DT, VEC, true>(S, P, row, s, pen, rep, pres, freq, k0,
+                                                          surv, thr - 1, true);
+            cut = r.comp;
+            T = r.excl + r.meas;
+            l1 = false;
+        } else {
+            T = Sv;
+        }
+        if (T == 0) {
+            const SelResult r = row_select<DT, VEC, false>(S, P, row, s, pen, rep, pres, freq, k0,
+                                                           Pred{0, 0, 0}, 0, false);
+            tok_comp = r.comp;
+        } else {
+            const u128 g = floor_mul_f64(a.uniform[row], T);
+            const SelResult r = row_select<DT, VEC, true>(S, P, row, s, pen, rep, pres, freq, k0,
+                                                          Pred{tau, 0, cut}, g, l1);
+            tok_comp = r.comp;
+        }
+        token = comp_idx(tok_comp);
+        if (a.tk_key && tid == 0) a.tk_key[row] = tk;
+        // the LDS candidates were overwritten: reload them for the logprobs below
+        if (lp > 0 && n <= kGCap) {
+            for (int t = 0; t < NT; ++t) {
+                const uint32_t o = S.coff[t], m = S.coff[t + 1] - o;
+                const uint64_t* src = P.w.cand + ((size_t)row * NT + t) * kCap;
+                for (uint32_t i = tid; i < m; i += kFinThreads)
+                    S.cand[o + i] = comp_key(fkey(y_of_xkey(comp_k(src[i]), s)), comp_idx(src[i]));
+            }
+            if (tid == 0) S.cand[n - 1] = comp_key(k0, 0);
+            __syncthreads();
+        }
+    }
+
+    // Logprobs (sampler.py:262-291, rule R7): chosen token, then the row's best L,
+    // all from the penalised, scaled distribution before filtering.
+    if (lp >= 0) {
+        if (tid == 0 && a.chosen_logprob)
+            a.chosen_logprob[row] = (float)(((double)key_to_float(comp_k(tok_comp)) - (double)M) - lse);
+        const int L = lp < a.lp_cols ? lp : a.lp_cols;
+        if (L > 0) {
+            bool ok = n >= L && n <= kGCap;
+            SelResult r{0, 0, 0, 0};
+            if (ok) {
+                r = lds_select<false>(S, n, Pred{0, 0, 0}, (u128)(L - 1));
+                ok = r.found && comp_k(r.comp) > safe;
+            }
+            if (!ok) {
+                r = row_select<DT, VEC, false>(S, P, row, s, pen, rep, pres, freq, k0,
+                                               Pred{0, 0, 0}, (u128)(L - 1), false);
+                n = pass_gather<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0,
+                                         Pred{0, 0, r.comp}, 64, 0);
+            }
+            // the L composites >= r.comp (exactly L of them), then sorted by one thread
+            if (tid == 0) S.bcnt = 0;
+            __syncthreads();
+            for (int i = tid; i < n; i += kFinThreads) {
+                const uint64_t c = S.cand[i];
+                if (c >= r.comp) {
+                    const uint32_t at = atomicAdd(&S.bcnt, 1u);
+                    if (at < 32) ((uint64_t*)S.hm_lo)[at] = c;
+                }
+            }
+            __syncthreads();
+            if (tid == 0) {
+                const int m = (int)(S.bcnt < 32 ? S.bcnt : 32);
+                uint64_t* top = (uint64_t*)S.hm_lo;
+                for (int i = 1; i < m; ++i) {
+                    const uint64_t c = top[i];
+                    int j = i;
+                    while (j > 0 && top[j - 1] < c) { top[j] = top[j - 1]; --j; }
+                    top[j] = c;
+                }
+                for (int j = 0; j < a.lp_cols; ++j) {
+                    const size_t o = (size_t)row * a.lp_cols + j;
+                    const bool have = j < m && j < L;
+                    if (a.top_ids) a.top_ids[o] = have ? (int64_t)comp_idx(top[j]) : -1;
+                    if (a.top_logprobs)
+                        a.top_logprobs[o] = have ? (float)(((double)key_to_float(comp_k(top[j])) - (double)M) - lse) : 0.0f;
+                }
+            }
+        } else if (tid == 0) {
+            for (int j = 0; j < a.lp_cols; ++j) {
+                const size_t o = (size_t)row * a.lp_cols + j;
+                if (a.top_ids) a.top_ids[o] = -1;
+                if (a.top_logprobs) a.top_logprobs[o] = 0.0f;
+            }
+        }
+    }
+
+    if (tid == 0) {
+        a.tokens[row] = token;
+        if (a.status) a.status[row] = status;
+        if (a.row_max) a.row_max[row] = M;
+        if (a.cut_comp) a.cut_comp[row] = cut;
+        if (greedy && a.tk_key) a.tk_key[row] = 0;
+        if (a.kept_mass) { a.kept_mass[2 * row] = (uint64_t)T; a.kept_mass[2 * row + 1] = (uint64_t)(T >> 64); }
+        if (a.row_mass) { a.row_mass[2 * row] = (uint64_t)sall; a.row_mass[2 * row + 1] = (uint64_t)(sall >> 64); }
+        RowRes rr;
+        rr.cut = cut;
+        rr.klo = (uint64_t)T;
+        rr.khi = (uint64_t)(T >> 64);
+        rr.tau = tau;
+        rr.greedy = greedy ? 1u : 0u;
+        rr.token = token;
+        rr.M = M;
+        rr.s = s;
+        P.w.res[row] = rr;
+    }
+}
+
+}  // namespace fie

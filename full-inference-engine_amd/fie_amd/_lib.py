@@ -13,11 +13,15 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_native", "libfie_sampler.so")
 
 FIE_OK = 0
+FIE_E_ARG, FIE_E_WORKSPACE, FIE_E_LAUNCH = -1, -2, -3
 FIE_F32, FIE_F16, FIE_BF16 = 0, 1, 2
-FIE_ROW_OVERFLOW = 1
-FIE_ROW_TIMEOUT = 2
-FIE_STAGE_PENALTY, FIE_STAGE_SAMPLE = 0, 1
+FIE_FLAG_GREEDY, FIE_FLAG_PENALTY = 1, 2
+FIE_ROW_EXACT_PATH = 1
+FIE_ROW_UNCOUNTED_IDS = 2
+FIE_STAGE_SCAN, FIE_STAGE_FINISH = 0, 1
 LP_COLS = 20
+TILE = 8192
+MAX_VOCAB = 64 * TILE
 
 _vp = ctypes.c_void_p
 
@@ -30,10 +34,9 @@ class SamplerArgs(ctypes.Structure):
         ("vocab", ctypes.c_int32), ("lp_cols", ctypes.c_int32), ("row_stride", ctypes.c_int64),
         ("scale", _vp), ("top_k", _vp), ("top_p", _vp), ("min_p", _vp), ("flags", _vp),
         ("logprobs", _vp), ("uniform", _vp),
-        ("apply_penalties", ctypes.c_int32), ("reserved0", ctypes.c_int32),
+        ("apply_penalties", ctypes.c_int32), ("max_row_hist", ctypes.c_int32),
         ("repetition", _vp), ("presence", _vp), ("frequency", _vp),
-        ("hist_offsets", _vp), ("hist_ids", _vp), ("hist_total", ctypes.c_int64),
-        ("epoch", ctypes.c_int64),
+        ("hist_offsets", _vp), ("hist_ids", _vp), ("hist_invalid", _vp),
         ("tokens", _vp), ("status", _vp), ("tk_key", _vp), ("cut_comp", _vp),
         ("row_max", _vp), ("kept_mass", _vp), ("row_mass", _vp), ("chosen_logprob", _vp),
         ("top_ids", _vp), ("top_logprobs", _vp),
@@ -44,14 +47,13 @@ class Workspace(ctypes.Structure):
     """Mirror of ``fie_workspace``."""
 
     _fields_ = [("ptr", _vp), ("bytes", ctypes.c_size_t), ("max_rows", ctypes.c_int32),
-                ("vocab", ctypes.c_int32), ("max_hist", ctypes.c_int64)]
+                ("vocab", ctypes.c_int32)]
 
 
+# Every symbol include/fie_sampler.h declares.
 EXPORTS = (
-    "fie_sampler_workspace_size", "fie_sampler_workspace_init", "fie_sampler_sample",
-    "fie_sampler_stage",
-    "fie_sampler_resolve_overflow", "fie_sampler_argmax", "fie_sampler_kept",
-    "fie_sampler_cexp", "fie_sampler_last_error", "fie_sampler_set_trace",
+    "fie_sampler_workspace_size", "fie_sampler_sample", "fie_sampler_stage",
+    "fie_sampler_argmax", "fie_sampler_kept", "fie_sampler_cexp", "fie_sampler_last_error",
 )
 
 _lib = None
@@ -72,27 +74,28 @@ def load():
         raise NativeError(
             f"the HIP sampler library is not built ({LIB_PATH}); run fie_amd.build.build()")
     lib = ctypes.CDLL(LIB_PATH)
+    bind(lib)
+    _lib = lib
+    return lib
+
+
+def bind(lib) -> None:
+    """Declare argument and result types of every exported function."""
     lib.fie_sampler_workspace_size.restype = ctypes.c_size_t
-    lib.fie_sampler_workspace_size.argtypes = [ctypes.c_int32, ctypes.c_int32, ctypes.c_int64]
-    lib.fie_sampler_workspace_init.argtypes = [ctypes.POINTER(Workspace), _vp]
+    lib.fie_sampler_workspace_size.argtypes = [ctypes.c_int32, ctypes.c_int32]
     lib.fie_sampler_sample.argtypes = [ctypes.POINTER(SamplerArgs), ctypes.POINTER(Workspace), _vp]
     lib.fie_sampler_stage.argtypes = [
         ctypes.POINTER(SamplerArgs), ctypes.POINTER(Workspace), ctypes.c_int32, _vp]
-    lib.fie_sampler_resolve_overflow.argtypes = [
-        ctypes.POINTER(SamplerArgs), _vp, ctypes.c_int32, ctypes.POINTER(Workspace), _vp]
     lib.fie_sampler_argmax.argtypes = [
         _vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, ctypes.c_int64, _vp,
         ctypes.POINTER(Workspace), _vp]
     lib.fie_sampler_kept.argtypes = [
         ctypes.POINTER(SamplerArgs), _vp, _vp, ctypes.POINTER(Workspace), _vp]
     lib.fie_sampler_cexp.argtypes = [_vp, _vp, ctypes.c_int64, _vp]
-    lib.fie_sampler_set_trace.argtypes = [_vp]
     lib.fie_sampler_last_error.restype = ctypes.c_char_p
     for name in EXPORTS:
         if name not in ("fie_sampler_workspace_size", "fie_sampler_last_error"):
             getattr(lib, name).restype = ctypes.c_int
-    _lib = lib
-    return lib
 
 
 def check(rc: int, what: str) -> None:

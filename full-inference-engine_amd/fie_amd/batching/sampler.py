@@ -30,6 +30,43 @@ class SampleResult:
     logprobs: dict[int, list[tuple[int, float]]]
 
 
+def pack_history(contexts: list[list[int]], include: np.ndarray, vocab: int):
+    """CSR of the penalty contexts of the rows in `include` (sampler.py:136-144 reads
+    only penalised rows), plus, per row, the ids >= vocab that the reference's
+    scatter sends to index 0 (sampler.py:156-157): their distinct count, and bit 30
+    when one of them first occurs after token 0's first occurrence."""
+    rows = len(contexts)
+    parts = [np.asarray(c, dtype=np.int64) if include[i] and len(c) else _EMPTY
+             for i, c in enumerate(contexts)]
+    lengths = np.fromiter((p.shape[0] for p in parts), dtype=np.int64, count=rows)
+    offsets = np.zeros(rows + 1, dtype=np.int64)
+    np.cumsum(lengths, out=offsets[1:])
+    flat = np.concatenate(parts) if offsets[-1] else _EMPTY
+    invalid = None
+    if flat.size:
+        if flat.min() < 0 or flat.max() >= 2**31:
+            raise ValueError("penalty context token ids must be in [0, 2**31)")
+        bad = flat >= vocab
+        if bad.any():
+            invalid = np.zeros(rows, dtype=np.int32)
+            for r in np.unique(np.searchsorted(offsets, np.nonzero(bad)[0], side="right") - 1):
+                ids = parts[r]
+                big, first = np.unique(ids[ids >= vocab], return_index=True)
+                value = int(big.size)
+                zero = np.nonzero(ids == 0)[0]
+                if zero.size:
+                    # first occurrences of the big ids, as positions in the row
+                    pos = np.nonzero(ids >= vocab)[0][first]
+                    if (pos > zero[0]).any():
+                        value |= 1 << 30
+                invalid[r] = value
+    longest = int(lengths.max()) if rows else 0
+    return offsets, flat.astype(np.int32), invalid, longest
+
+
+_EMPTY = np.zeros(0, dtype=np.int64)
+
+
 def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarray,
                    contexts: list[list[int]] | None) -> HostParams:
     """Per-row arrays for the kernels, derived the way sampler.py:109,182-192 does."""
@@ -43,19 +80,10 @@ def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarra
     lp = np.fromiter((-1 if p.logprobs is None else p.logprobs for p in params),
                      dtype=np.int32, count=rows)
     apply = bool(pen.any()) and contexts is not None
-    offsets = np.zeros(rows + 1, dtype=np.int64)
-    ids = np.zeros(0, dtype=np.int32)
     if apply:
-        # Only penalised rows' contexts are read (sampler.py:136-139).
-        lengths = np.fromiter((len(c) if pen[i] else 0 for i, c in enumerate(contexts)),
-                              dtype=np.int64, count=rows)
-        np.cumsum(lengths, out=offsets[1:])
-        if offsets[-1]:
-            flat = np.fromiter((t for i, c in enumerate(contexts) if pen[i] for t in c),
-                               dtype=np.int64, count=int(offsets[-1]))
-            if flat.min() < 0 or flat.max() >= 2**31:
-                raise ValueError("penalty context token ids must be in [0, 2**31)")
-            ids = flat.astype(np.int32)
+        offsets, ids, invalid, longest = pack_history(contexts, pen, vocab)
+    else:
+        offsets, ids, invalid, longest = np.zeros(rows + 1, np.int64), _EMPTY.astype(np.int32), None, 0
     return HostParams(
         scale=np.where(greedy, 1.0, temps).astype(np.float32),
         top_k=np.where((top_k > 0) & (top_k < vocab) & ~greedy, top_k, 0).astype(np.int32),
@@ -70,6 +98,8 @@ def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarra
         hist_off=offsets,
         hist_ids=ids,
         apply_penalties=apply,
+        hist_invalid=invalid,
+        max_row_hist=longest,
     )
 
 

@@ -1,25 +1,35 @@
 /*
- * TEST INFRASTRUCTURE ONLY.  Nothing in the product may load or call this file.
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product may load or call this file;
+ * only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it, and
+ * only as the checker.
  *
  * Plain-C restatement of the reference token sampler
  *   engine/batching/sampler.py:81-291  (BatchedSampler.sample and its stages)
  *   engine/runtime/sampling.py:71-79   (greedy / has_penalties predicates)
- * written as the checker for the HIP sampler.  Every stage follows the reference
- * line it cites; the places where the reference leaves the result to ATen's float
- * rounding (top-p boundary bits, tie order under an unstable sort, the multinomial
- * stream) are replaced by the build's canonical rules, stated where they are used:
+ * written as the checker for the HIP sampler.  Each stage follows the reference
+ * line it cites.  Where the reference leaves a result to ATen's float rounding
+ * (the fp32 bits of softmax and cumsum that decide a top-p boundary, the tie order
+ * of an unstable sort, the torch.multinomial stream), the build's canonical rules
+ * replace it:
  *
- *   (R1) weights     W_i = floor(cexp(y_i - M) * 2^40), an integer; all mass sums
- *                    are exact 64-bit integer sums, so no summation order matters.
- *   (R2) order       tokens are ranked by (y descending, token index ascending).
- *   (R3) top-p       token at rank j is dropped iff  sum_{rank<j} W >= p * S,
- *                    evaluated exactly (p is the fp32 value of top_p).
- *   (R4) draw        t = floor(u * T) with T the kept mass; the token is the first
- *                    kept token in (R2) order whose inclusive prefix mass exceeds t.
- *   (R5) min-p       token dropped iff cexp(y_i - M) < fp32(min_p).
- *   (R6) top_p == 1  drops nothing (the exact-arithmetic reading of the reference's
- *                    `cumulative - p >= 1.0` test, sampler.py:226).
- *   (R7) logprobs    lse = M + ln(S_all / 2^40), S_all the weight sum over the row.
+ *   (R1) weights   The row is cut into tiles: token 0 alone, then
+ *                  [1, T), [T, 2T), ... with T = FIE_TILE.  m_t is the largest
+ *                  scaled logit of tile t and M the largest of the row.
+ *                    W_i = floor(cexp(y_i - m_t) * 2^40)      (token weight)
+ *                    C_t = floor(cexp(m_t - M)  * 2^40)      (tile scale)
+ *                    w_i = W_i * C_t                          (row weight, < 2^81)
+ *                  Every mass is an exact integer sum of w_i, so no summation
+ *                  order matters, and a tile's sums need only its own maximum.
+ *   (R2) order     tokens rank by (y descending, token index ascending).
+ *   (R3) top-p     the token at rank j is dropped iff  sum_{rank<j} w >= ceil(p*S)
+ *                  (S = mass of the top-k/min-p survivors, p the fp32 top_p),
+ *                  evaluated exactly.
+ *   (R4) draw      t = floor(u * K) with K the kept mass; the token is the first
+ *                  kept token in (R2) order whose inclusive prefix mass exceeds t.
+ *   (R5) min-p     a token is dropped iff cexp(y_i - M) < fp32(min_p).
+ *   (R6) top_p==1  drops nothing (the exact-arithmetic reading of the reference's
+ *                  `cumulative - p >= 1.0` test, sampler.py:226).
+ *   (R7) logprobs  lse = M + ln(S_all) - 80 ln 2, S_all the mass of the whole row.
  *
  * cexp() is the build's own fp32 exponential: Cody-Waite reduction by ln 2 (split
  * constant), a degree-7 Taylor polynomial for e^r on |r| <= ln2/2 evaluated by
@@ -32,6 +42,9 @@
 #include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
+
+#define FIE_TILE 8192
+typedef unsigned __int128 u128;
 
 /* ------------------------------------------------------------------ arithmetic */
 
@@ -53,7 +66,23 @@ float oracle_cexp(float d)
     return ldexpf(p, (int)n);
 }
 
-static inline uint64_t weight_of(float e)
+/* cexp() over every fp32 d in [lo, hi] (bit patterns walked in order): returns the
+ * number of adjacent pairs where the result decreases as d increases. */
+int64_t oracle_cexp_monotone_violations(float lo, float hi)
+{
+    int64_t bad = 0;
+    float prev = oracle_cexp(lo);
+    float d = lo;
+    while (d < hi) {
+        d = nextafterf(d, hi);
+        float e = oracle_cexp(d);
+        if (e < prev) ++bad;
+        prev = e;
+    }
+    return bad;
+}
+
+static inline uint64_t fixed40(float e)
 {
     return (uint64_t)((double)e * 1099511627776.0);   /* floor(e * 2^40), exact */
 }
@@ -83,31 +112,57 @@ static int cmp_desc_u64(const void* a, const void* b)
     return (x < y) - (x > y);
 }
 
-/* ceil(p * S) for fp32 p in (0,1) and integer S < 2^63, exactly. */
-static uint64_t ceil_mul_f32(float p, uint64_t S)
+/* floor(m * X / 2^q) for m < 2^53, X < 2^128, exactly (a 192-bit product). */
+static u128 mul_shift(uint64_t m, u128 X, int q)
 {
-    int e;
-    float m = frexpf(p, &e);                     /* p = m * 2^e, m in [0.5,1) */
-    uint64_t mi = (uint64_t)ldexpf(m, 24);       /* 24-bit integer mantissa */
-    int q = 24 - e;                              /* p = mi / 2^q, q >= 24 */
-    unsigned __int128 prod = (unsigned __int128)mi * S;
-    if (q >= 127) return prod ? 1 : 0;
-    unsigned __int128 fl = prod >> q;
-    unsigned __int128 rem = prod - (fl << q);
-    return (uint64_t)(fl + (rem ? 1 : 0));
+    u128 lo = (u128)m * (uint64_t)X;                     /* < 2^117 */
+    u128 hi = (u128)m * (uint64_t)(X >> 64);             /* < 2^117 */
+    /* product = hi * 2^64 + lo = P2 * 2^128 + P1 * 2^64 + P0 */
+    uint64_t p0 = (uint64_t)lo;
+    u128 mid = (lo >> 64) + hi;                          /* < 2^118 */
+    uint64_t p1 = (uint64_t)mid;
+    uint64_t p2 = (uint64_t)(mid >> 64);
+    if (q >= 192) return 0;
+    if (q >= 128) return (u128)(p2 >> (q - 128));
+    if (q >= 64) {
+        int s = q - 64;
+        u128 v = ((u128)p2 << 64) | p1;
+        return s ? (v >> s) : v;
+    }
+    u128 v = ((u128)p1 << 64) | p0;
+    return q ? ((v >> q) | ((u128)p2 << (128 - q))) : v;
 }
 
-/* floor(u * T) for double u in [0,1) and integer T < 2^63, exactly. */
-static uint64_t floor_mul_f64(double u, uint64_t T)
+/* Exact ceil(p * S) for an fp32 p in (0, 1) and S < 2^104 (so p's 24-bit
+ * mantissa times S fits in 128 bits). */
+static u128 ceil_mul_f32(float p, u128 S)
+{
+    uint32_t b;
+    memcpy(&b, &p, 4);
+    uint32_t eb = (b >> 23) & 0xFFu;
+    uint64_t mant = (b & 0x7FFFFFu) | (eb ? 0x800000u : 0u);
+    int q = eb ? 150 - (int)eb : 149;                    /* p = mant / 2^q, q >= 24 */
+    u128 P = (u128)mant * S;
+    if (q >= 128) return P ? 1 : 0;
+    return (P >> q) + (((P & ((((u128)1) << q) - 1)) != 0) ? 1 : 0);
+}
+
+/* Exact floor(u * K) for a double u in [0, 1) and K < 2^104. */
+static u128 floor_mul_f64(double u, u128 K)
 {
     if (!(u > 0.0)) return 0;
-    int e;
-    double m = frexp(u, &e);                     /* u = m * 2^e */
-    uint64_t mi = (uint64_t)ldexp(m, 53);
-    int q = 53 - e;                              /* u = mi / 2^q, q >= 53 */
-    unsigned __int128 prod = (unsigned __int128)mi * T;
-    if (q >= 127) return 0;
-    return (uint64_t)(prod >> q);
+    uint64_t b;
+    memcpy(&b, &u, 8);
+    uint32_t eb = (uint32_t)((b >> 52) & 0x7FFu);
+    uint64_t mant = (b & 0xFFFFFFFFFFFFFull) | (eb ? (1ull << 52) : 0ull);
+    int q = eb ? 1075 - (int)eb : 1074;                  /* u = mant / 2^q */
+    return mul_shift(mant, K, q);
+}
+
+/* u128 -> double as hi * 2^64 + lo, both conversions and the add in double. */
+static double u128_to_double(u128 x)
+{
+    return (double)(uint64_t)(x >> 64) * 18446744073709551616.0 + (double)(uint64_t)x;
 }
 
 /* ------------------------------------------------------------------ penalties */
@@ -150,10 +205,11 @@ static int32_t unique_in_order(const int32_t* ids, int64_t n, uniq_t* out, occ_t
  * _apply_penalties, sampler.py:120-175, in place on w[B*V].
  * The gather reads the unpenalised logits; the scatter then writes, for every row,
  * `width` entries in column order (real entries first, pad entries after), and a
- * later write to the same index replaces an earlier one, as a sequential scatter
- * does.  Pad entries and ids >= V target index 0 with the original logit of token 0
- * (sampler.py:156-157,174), which is how a real token-0 penalty can be undone (Q1).
- * Returns the batch width, or -1 on a negative id.
+ * later write to the same index replaces an earlier one, as a sequential CPU
+ * scatter does.  Pad entries and ids >= V target index 0 with the original logit of
+ * token 0 (sampler.py:156-157,174), which is how a real token-0 penalty can be
+ * undone (Q1).  Rows without penalties or with an empty context contribute no
+ * entries (sampler.py:136-139).  Returns the batch width, or -1 on a negative id.
  */
 int32_t oracle_penalize(float* w, int32_t B, int32_t V, const uint8_t* has_pen,
                         const float* rep, const float* pres, const float* freq,
@@ -178,12 +234,12 @@ int32_t oracle_penalize(float* w, int32_t B, int32_t V, const uint8_t* has_pen,
         if (nu[r] > width) width = nu[r];
     }
     if (width > 0) {
+        float* src = malloc((size_t)width * sizeof(float));
+        int32_t* dst = malloc((size_t)width * sizeof(int32_t));
         for (int32_t r = 0; r < B; ++r) {
             float* row = w + (int64_t)r * V;
             float g0 = row[0];
             /* gather every value first: the scatter source is built from the input */
-            float* src = malloc((size_t)width * sizeof(float));
-            int32_t* dst = malloc((size_t)width * sizeof(int32_t));
             for (int32_t j = 0; j < width; ++j) {
                 if (j < nu[r] && rows[r][j].id < V) {
                     float g = row[rows[r][j].id];
@@ -198,8 +254,8 @@ int32_t oracle_penalize(float* w, int32_t B, int32_t V, const uint8_t* has_pen,
                 }
             }
             for (int32_t j = 0; j < width; ++j) row[dst[j]] = src[j];
-            free(src); free(dst);
         }
+        free(src); free(dst);
     }
     for (int32_t r = 0; r < B; ++r) free(rows[r]);
     free(rows); free(nu); free(tmp);
@@ -226,11 +282,11 @@ typedef struct {
     int32_t lp_cols;               /* columns of top_ids/top_lp */
     /* outputs */
     int64_t* tokens;               /* [B] */
-    uint32_t* tk_key;              /* [B] top-k threshold key (0 = none) */
-    uint64_t* cut_comp;            /* [B] composite key of the last top-p survivor (0 = none) */
+    uint32_t* tk_key;              /* [B] key of the top-k threshold value (0 = none) */
+    uint64_t* cut_comp;            /* [B] composite of the last top-p survivor (0 = none) */
     float* row_max;                /* [B] M */
-    uint64_t* t_kept;              /* [B] kept mass */
-    uint64_t* s_all;               /* [B] whole-row mass */
+    uint64_t* kept_mass;           /* [B*2] kept mass, low and high 64 bits */
+    uint64_t* row_mass;            /* [B*2] whole-row mass, low and high 64 bits */
     uint8_t* kept;                 /* [B*V] or NULL */
     float* probs;                  /* [B*V] or NULL */
     float* chosen_lp;              /* [B] or NULL */
@@ -238,35 +294,59 @@ typedef struct {
     float* top_lp;                 /* [B*lp_cols] or NULL */
 } oracle_args;
 
+static inline int tile_of(int32_t i) { return i == 0 ? 0 : 1 + i / FIE_TILE; }
+
 int32_t oracle_sample(oracle_args* a)
 {
     const int32_t B = a->B, V = a->V;
+    if (V <= 0 || V >= (1 << 24)) return -2;
     if (a->apply_penalties) {
         if (oracle_penalize(a->logits, B, V, a->has_pen, a->rep, a->pres, a->freq,
                             a->hist_off, a->hist_ids) < 0) return -1;
     }
+    const int NTS = 2 + (V - 1) / FIE_TILE;             /* tile slots incl. token 0 */
     float* y = malloc((size_t)V * sizeof(float));
-    float* e = malloc((size_t)V * sizeof(float));
+    u128* w = malloc((size_t)V * sizeof(u128));
     uint64_t* order = malloc((size_t)V * sizeof(uint64_t));
     uint8_t* surv = malloc((size_t)V);
+    uint32_t* tmax = malloc((size_t)NTS * sizeof(uint32_t));
+    uint64_t* tC = malloc((size_t)NTS * sizeof(uint64_t));
     for (int32_t r = 0; r < B; ++r) {
-        const float* w = a->logits + (int64_t)r * V;
+        const float* xr = a->logits + (int64_t)r * V;
         const float s = a->scale[r];
         /* _apply_temperature, sampler.py:177-185: a true fp32 divide per element */
+        for (int t = 0; t < NTS; ++t) tmax[t] = 0;      /* 0 = empty tile */
         uint32_t best = 0;
         int32_t amax = 0;
         for (int32_t i = 0; i < V; ++i) {
-            y[i] = w[i] / s + 0.0f;                  /* +0.0f folds -0 into +0 */
-            if (i == 0 || fkey(y[i]) > best) { best = fkey(y[i]); amax = i; }
+            y[i] = xr[i] / s + 0.0f;                     /* +0.0f folds -0 into +0 */
+            uint32_t k = fkey(y[i]);
+            if (i == 0 || k > best) { best = k; amax = i; }
+            int t = tile_of(i);
+            if (k > tmax[t]) tmax[t] = k;      /* keys of non-NaN values are never 0 */
         }
         const float M = y[amax];
         a->row_max[r] = M;
-        uint64_t sall = 0;
-        for (int32_t i = 0; i < V; ++i) {
-            e[i] = oracle_cexp(y[i] - M);
-            sall += weight_of(e[i]);
+        /* (R1) tile scales and row weights */
+        for (int t = 0; t < NTS; ++t) {
+            if (tmax[t] == 0) { tC[t] = 0; continue; }
+            uint32_t kt = tmax[t];
+            uint32_t bits = (kt & 0x80000000u) ? (kt & 0x7FFFFFFFu) : ~kt;
+            float mt;
+            memcpy(&mt, &bits, 4);
+            tC[t] = fixed40(oracle_cexp(mt - M));
         }
-        a->s_all[r] = sall;
+        u128 sall = 0;
+        for (int32_t i = 0; i < V; ++i) {
+            uint32_t kt = tmax[tile_of(i)];
+            uint32_t bits = (kt & 0x80000000u) ? (kt & 0x7FFFFFFFu) : ~kt;
+            float mt;
+            memcpy(&mt, &bits, 4);
+            w[i] = (u128)fixed40(oracle_cexp(y[i] - mt)) * tC[tile_of(i)];
+            sall += w[i];
+        }
+        a->row_mass[2 * r] = (uint64_t)sall;
+        a->row_mass[2 * r + 1] = (uint64_t)(sall >> 64);
         a->tk_key[r] = 0;
         a->cut_comp[r] = 0;
         int need_sort = a->greedy[r] ? (a->logprobs[r] > 0) : 1;
@@ -274,10 +354,11 @@ int32_t oracle_sample(oracle_args* a)
             for (int32_t i = 0; i < V; ++i) order[i] = comp_of(y[i], i);
             qsort(order, (size_t)V, sizeof(uint64_t), cmp_desc_u64);
         }
+        u128 T = 0;
         if (a->greedy[r]) {
             /* _draw greedy rows, sampler.py:236-238: argmax, first index on ties */
             a->tokens[r] = amax;
-            a->t_kept[r] = weight_of(1.0f);
+            T = w[amax];
             if (a->kept) memset(a->kept + (int64_t)r * V, 1, (size_t)V);
             if (a->probs) {
                 memset(a->probs + (int64_t)r * V, 0, (size_t)V * sizeof(float));
@@ -292,47 +373,52 @@ int32_t oracle_sample(oracle_args* a)
             }
             /* _filter min-p, sampler.py:211-218, rule (R5) */
             const float mp = a->min_p[r];
-            uint64_t S = 0;
+            u128 S = 0;
             for (int32_t i = 0; i < V; ++i) {
-                surv[i] = (fkey(y[i]) >= tk) && !(mp > 0.0f && e[i] < mp);
-                if (surv[i]) S += weight_of(e[i]);
+                surv[i] = (fkey(y[i]) >= tk) && !(mp > 0.0f && oracle_cexp(y[i] - M) < mp);
+                if (surv[i]) S += w[i];
             }
             /* _filter top-p, sampler.py:220-228, rules (R2)(R3)(R6) */
             const float p = a->top_p[r];
-            uint64_t T = 0;
-            uint64_t thr = (p < 1.0f) ? ceil_mul_f32(p, S) : UINT64_MAX;
-            uint64_t excl = 0;
-            int stopped = 0;
-            for (int32_t j = 0; j < V; ++j) {
-                int32_t i = idx_of(order[j]);
-                if (!surv[i]) continue;
-                if (stopped || excl >= thr) { stopped = 1; surv[i] = 0; continue; }
-                excl += weight_of(e[i]);
-                if (p < 1.0f) a->cut_comp[r] = order[j];
+            if (p < 1.0f) {
+                u128 thr = ceil_mul_f32(p, S);
+                u128 excl = 0;
+                int stopped = 0;
+                for (int32_t j = 0; j < V; ++j) {
+                    int32_t i = idx_of(order[j]);
+                    if (!surv[i]) continue;
+                    if (stopped || excl >= thr) { stopped = 1; surv[i] = 0; continue; }
+                    excl += w[i];
+                    a->cut_comp[r] = order[j];
+                }
             }
-            for (int32_t i = 0; i < V; ++i) if (surv[i]) T += weight_of(e[i]);
-            a->t_kept[r] = T;
+            for (int32_t i = 0; i < V; ++i) if (surv[i]) T += w[i];
             /* _draw sampled rows, sampler.py:241-259, replaced by rule (R4) */
-            uint64_t t = floor_mul_f64(a->uniform[r], T);
-            uint64_t incl = 0;
-            int64_t tok = -1;
-            for (int32_t j = 0; j < V; ++j) {
-                int32_t i = idx_of(order[j]);
-                if (!surv[i]) continue;
-                incl += weight_of(e[i]);
-                if (incl > t) { tok = i; break; }
+            int64_t tok = amax;
+            if (T > 0) {
+                u128 t = floor_mul_f64(a->uniform[r], T);
+                u128 incl = 0;
+                for (int32_t j = 0; j < V; ++j) {
+                    int32_t i = idx_of(order[j]);
+                    if (!surv[i]) continue;
+                    incl += w[i];
+                    if (incl > t) { tok = i; break; }
+                }
             }
             a->tokens[r] = tok;
             if (a->kept) for (int32_t i = 0; i < V; ++i) a->kept[(int64_t)r * V + i] = surv[i];
             if (a->probs) {
+                double Td = u128_to_double(T);
                 for (int32_t i = 0; i < V; ++i)
                     a->probs[(int64_t)r * V + i] =
-                        surv[i] ? (float)((double)e[i] * 1099511627776.0 / (double)T) : 0.0f;
+                        (surv[i] && T > 0) ? (float)(u128_to_double(w[i]) / Td) : 0.0f;
             }
         }
+        a->kept_mass[2 * r] = (uint64_t)T;
+        a->kept_mass[2 * r + 1] = (uint64_t)(T >> 64);
         /* _logprobs, sampler.py:262-291, rule (R7) */
         if (a->logprobs[r] >= 0) {
-            double lse = log((double)sall / 1099511627776.0);
+            double lse = log(u128_to_double(sall)) - 80.0 * 0.69314718055994530942;
             if (a->chosen_lp) {
                 int64_t c = a->tokens[r];
                 a->chosen_lp[r] = (float)(((double)y[c] - (double)M) - lse);
@@ -352,6 +438,6 @@ int32_t oracle_sample(oracle_args* a)
             }
         }
     }
-    free(y); free(e); free(order); free(surv);
+    free(y); free(w); free(order); free(surv); free(tmax); free(tC);
     return 0;
 }

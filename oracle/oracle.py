@@ -49,7 +49,14 @@ def _load():
         _lib.oracle_sample.restype = ctypes.c_int32
         _lib.oracle_sample.argtypes = [ctypes.c_void_p]
         _lib.oracle_penalize.restype = ctypes.c_int32
+        _lib.oracle_cexp_monotone_violations.restype = ctypes.c_int64
+        _lib.oracle_cexp_monotone_violations.argtypes = [ctypes.c_float, ctypes.c_float]
     return _lib
+
+
+def cexp_monotone_violations(lo: float, hi: float) -> int:
+    """Adjacent fp32 pairs in [lo, hi] where the canonical exponential decreases."""
+    return int(_load().oracle_cexp_monotone_violations(lo, hi))
 
 
 def cexp(values: np.ndarray) -> np.ndarray:
@@ -136,7 +143,7 @@ class _Args(ctypes.Structure):
         ("freq", ctypes.c_void_p), ("hist_off", ctypes.c_void_p), ("hist_ids", ctypes.c_void_p),
         ("lp_cols", ctypes.c_int32),
         ("tokens", ctypes.c_void_p), ("tk_key", ctypes.c_void_p), ("cut_comp", ctypes.c_void_p),
-        ("row_max", ctypes.c_void_p), ("t_kept", ctypes.c_void_p), ("s_all", ctypes.c_void_p),
+        ("row_max", ctypes.c_void_p), ("kept_mass", ctypes.c_void_p), ("row_mass", ctypes.c_void_p),
         ("kept", ctypes.c_void_p), ("probs", ctypes.c_void_p), ("chosen_lp", ctypes.c_void_p),
         ("top_ids", ctypes.c_void_p), ("top_lp", ctypes.c_void_p),
     ]
@@ -148,8 +155,8 @@ class CanonicalResult:
     tk_key: np.ndarray
     cut_comp: np.ndarray
     row_max: np.ndarray
-    t_kept: np.ndarray
-    s_all: np.ndarray
+    kept_mass: np.ndarray    # uint64 [B, 2]: low and high 64 bits
+    row_mass: np.ndarray     # uint64 [B, 2]
     kept: np.ndarray | None
     probs: np.ndarray | None
     chosen_lp: np.ndarray
@@ -177,7 +184,7 @@ def canonical_step(logits: np.ndarray, res: Resolved, uniform: np.ndarray,
     out = CanonicalResult(
         tokens=np.zeros(B, np.int64), tk_key=np.zeros(B, np.uint32),
         cut_comp=np.zeros(B, np.uint64), row_max=np.zeros(B, np.float32),
-        t_kept=np.zeros(B, np.uint64), s_all=np.zeros(B, np.uint64),
+        kept_mass=np.zeros((B, 2), np.uint64), row_mass=np.zeros((B, 2), np.uint64),
         kept=np.zeros((B, V), np.uint8) if want_kept else None,
         probs=np.zeros((B, V), np.float32) if want_kept else None,
         chosen_lp=np.zeros(B, np.float32),
@@ -193,12 +200,14 @@ def canonical_step(logits: np.ndarray, res: Resolved, uniform: np.ndarray,
         has_pen=_ptr(res.has_pen), rep=_ptr(res.rep), pres=_ptr(res.pres), freq=_ptr(res.freq),
         hist_off=_ptr(off), hist_ids=_ptr(ids) if ids.size else None, lp_cols=lp_cols,
         tokens=_ptr(out.tokens), tk_key=_ptr(out.tk_key), cut_comp=_ptr(out.cut_comp),
-        row_max=_ptr(out.row_max), t_kept=_ptr(out.t_kept), s_all=_ptr(out.s_all),
+        row_max=_ptr(out.row_max), kept_mass=_ptr(out.kept_mass), row_mass=_ptr(out.row_mass),
         kept=_ptr(out.kept), probs=_ptr(out.probs), chosen_lp=_ptr(out.chosen_lp),
         top_ids=_ptr(out.top_ids), top_lp=_ptr(out.top_lp),
     )
     rc = lib.oracle_sample(ctypes.byref(a))
     del keep
+    if rc == -2:
+        raise ValueError("vocab must be in [1, 2**24)")
     if rc != 0:
         raise ValueError("negative token id in a penalty context")
     return out

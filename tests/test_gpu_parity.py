@@ -1,0 +1,323 @@
+"""Parity of the HIP sampler with the canonical C oracle, on an MI355X.
+
+Every comparison is bit-exact for integer and index outputs (tokens, top-k key,
+top-p cut, kept mask, row maximum, kept and whole-row masses); normalised
+probabilities are checked to 1e-5 relative (the north-star tolerance for fp32).
+The workloads are the five BASELINE configurations (fie_amd/workloads.py): row
+subsets spanning every parameter class at full vocabulary, and whole batches.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from fie_amd import _lib
+from fie_amd import workloads as W
+from fie_amd.batching.sampler import BatchedSampler, resolve_params
+from fie_amd.kernel import FusedSampler
+from fie_amd.runtime.sampling import SamplingParams
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+PROB_RTOL = 1e-5
+
+
+@pytest.fixture(scope="module")
+def fs():
+    return FusedSampler(DEV)
+
+
+def _needs_mass(params):
+    return np.array([(p.logprobs is not None) or (not p.greedy and not (0 < p.top_k))
+                     for p in params])
+
+
+def run_both(fs, logits, params, uniforms, contexts=None, kept=True):
+    V = logits.shape[1]
+    print(f"  case: rows={logits.shape[0]} vocab={V} dtype={logits.dtype}", flush=True)
+    hp = resolve_params(params, V, uniforms, contexts)
+    out, args, _ = fs.step(logits.to(DEV), hp)
+    ref = O.canonical_step(logits.float().cpu().numpy(), O.resolve(params, V), uniforms,
+                           contexts=contexts, want_kept=kept)
+    gk = gp = None
+    if kept:
+        gk, gp = fs.kept(args)
+        torch.cuda.synchronize()
+        gk, gp = gk.cpu().numpy(), gp.cpu().numpy()
+    return out, ref, gk, gp
+
+
+def check(out, ref, params, gk=None, gp=None, lp=False):
+    np.testing.assert_array_equal(out["tokens"], ref.tokens, err_msg="tokens")
+    np.testing.assert_array_equal(out["row_max"].view(np.uint32), ref.row_max.view(np.uint32),
+                                  err_msg="row max")
+    np.testing.assert_array_equal(out["tk_key"], ref.tk_key, err_msg="top-k threshold key")
+    np.testing.assert_array_equal(out["cut_comp"], ref.cut_comp, err_msg="top-p cut")
+    np.testing.assert_array_equal(out["kept_mass"], ref.kept_mass, err_msg="kept mass")
+    m = _needs_mass(params)
+    np.testing.assert_array_equal(out["row_mass"][m], ref.row_mass[m], err_msg="row mass")
+    if gk is not None:
+        np.testing.assert_array_equal(gk, ref.kept, err_msg="kept set")
+        np.testing.assert_allclose(gp, ref.probs, rtol=PROB_RTOL, atol=0, err_msg="probs")
+    if lp:
+        want = np.array([p.logprobs is not None for p in params])
+        np.testing.assert_allclose(out["chosen_lp"][want], ref.chosen_lp[want], rtol=1e-6, atol=1e-6)
+        np.testing.assert_array_equal(out["top_ids"][want], ref.top_ids[want])
+        np.testing.assert_allclose(out["top_lp"][want], ref.top_lp[want], rtol=1e-6, atol=1e-6)
+
+
+SUBSETS = {
+    1: list(range(8)),
+    2: list(range(12)),
+    3: [0, 1, 2, 3, 64, 65, 66, 67, 128, 129, 130, 131, 192, 193, 194, 195],
+    4: list(range(8)),
+    5: list(range(16)),
+}
+
+
+@pytest.mark.parametrize("config", [1, 2, 3, 4, 5])
+def test_config_subset_bit_exact(fs, config):
+    w = W.make(config, rows=SUBSETS[config])
+    out, ref, gk, gp = run_both(fs, w.logits, w.params, w.uniforms, w.contexts)
+    check(out, ref, w.params, gk, gp)
+
+
+@pytest.mark.parametrize("config", [1, 2, 3, 5])
+def test_config_full_batch_bit_exact(fs, config):
+    w = W.make(config)
+    out, ref, _, _ = run_both(fs, w.logits, w.params, w.uniforms, w.contexts, kept=False)
+    check(out, ref, w.params)
+
+
+def test_c4_full_batch_properties(fs):
+    """C4 at full size (1024 rows): every token inside its own kept set, kept masses
+    positive, and a 64-row sample bit-exact against the oracle."""
+    w = W.make(4)
+    hp = resolve_params(w.params, w.logits.shape[1], w.uniforms, None)
+    out, args, _ = fs.step(w.logits.to(DEV), hp)
+    kept, _ = fs.kept(args, want_probs=False)
+    tok = torch.as_tensor(out["tokens"], device=DEV)
+    assert bool(kept.gather(1, tok.unsqueeze(1)).all())
+    assert (out["kept_mass"][:, 0] | out["kept_mass"][:, 1]).all()
+    rows = list(range(0, 1024, 16))
+    ref = O.canonical_step(w.logits[rows].float().cpu().numpy(), O.resolve(
+        [w.params[r] for r in rows], w.logits.shape[1]), w.uniforms[rows])
+    np.testing.assert_array_equal(out["tokens"][rows], ref.tokens)
+    np.testing.assert_array_equal(out["cut_comp"][rows], ref.cut_comp)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_argmax_first_index_on_ties(fs, dtype):
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(37, 151936, generator=g).to(dtype)
+    x[3, 100] = x[3, 90000] = 50.0          # tie: the first index wins
+    x[5, :] = 1.0                            # all equal
+    x[6, 151935] = 60.0                      # last index
+    x[7, 0] = 70.0                           # first index
+    got = fs.argmax(x.to(DEV)).cpu().numpy()
+    want = np.argmax(x.float().numpy(), axis=1)
+    np.testing.assert_array_equal(got, want)
+
+
+def _mixed_params(rows, vocab, rng, with_lp=True):
+    ps = []
+    for i in range(rows):
+        kind = i % 8
+        lp = int(rng.integers(0, 21)) if with_lp and i % 3 == 0 else None
+        if kind == 0:
+            ps.append(SamplingParams(logprobs=lp))
+        elif kind == 1:
+            ps.append(SamplingParams(temperature=0.8, top_k=int(rng.integers(2, 60)), logprobs=lp,
+                                     repetition_penalty=1.3, presence_penalty=0.2))
+        elif kind == 2:
+            ps.append(SamplingParams(temperature=1.3, top_p=float(rng.uniform(0.3, 0.99)),
+                                     frequency_penalty=0.4, logprobs=lp))
+        elif kind == 3:
+            ps.append(SamplingParams(temperature=0.5, top_k=int(rng.integers(2, 200)),
+                                     top_p=0.9, logprobs=lp))
+        elif kind == 4:
+            ps.append(SamplingParams(temperature=1.0, min_p=float(rng.uniform(0.01, 0.3)),
+                                     logprobs=lp, repetition_penalty=0.8))
+        elif kind == 5:
+            ps.append(SamplingParams(temperature=2.0, logprobs=lp))
+        elif kind == 6:
+            ps.append(SamplingParams(temperature=0.7, top_k=vocab + 5, top_p=0.5,
+                                     presence_penalty=-1.0, logprobs=lp))
+        else:
+            ps.append(SamplingParams(temperature=1.1, top_k=1, repetition_penalty=1.5))
+    return ps
+
+
+@pytest.mark.parametrize("vocab", [1, 7, 100, 8191, 8192, 8193, 20001])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_edge_shapes(fs, vocab, dtype):
+    rng = np.random.default_rng(vocab * 7 + int(dtype == torch.float16))
+    rows = 9
+    x = torch.from_numpy(rng.normal(0, 2.0, (rows, vocab)).astype(np.float32)).to(dtype)
+    params = _mixed_params(rows, vocab, rng)
+    ctx = [list(rng.integers(0, vocab + 3, size=int(rng.integers(0, 40)))) + ([0] if r % 2 else [])
+           for r in range(rows)]
+    out, ref, gk, gp = run_both(fs, x, params, rng.random(rows), ctx)
+    check(out, ref, params, gk, gp, lp=True)
+
+
+def test_unaligned_rows_take_the_scalar_path(fs):
+    rng = np.random.default_rng(11)
+    rows, vocab = 6, 30001
+    big = torch.from_numpy(rng.normal(0, 1.5, (rows, vocab + 1)).astype(np.float32)).half()
+    x = big[:, :vocab]                                   # row stride vocab + 1
+    assert x.stride(0) == vocab + 1
+    params = _mixed_params(rows, vocab, rng)
+    out, ref, gk, gp = run_both(fs, x, params, rng.random(rows), None)
+    check(out, ref, params, gk, gp, lp=True)
+
+
+def test_exact_path_rows(fs):
+    """Rows whose answer lies outside the streamed candidates: a wide top-k, a deep
+    nucleus on flat logits, plain temperature sampling and min-p on flat logits."""
+    rng = np.random.default_rng(5)
+    rows, vocab = 8, 151936
+    x = torch.from_numpy(rng.normal(0, 0.2, (rows, vocab)).astype(np.float32)).to(torch.bfloat16)
+    params = [SamplingParams(temperature=1.0, top_k=5000),
+              SamplingParams(temperature=1.0, top_p=0.99),
+              SamplingParams(temperature=1.0),
+              SamplingParams(temperature=1.0, min_p=0.5, logprobs=20),
+              SamplingParams(temperature=0.9, top_k=3000, top_p=0.97, logprobs=3),
+              SamplingParams(temperature=1.7, top_p=0.999),
+              SamplingParams(logprobs=5),
+              SamplingParams(temperature=1.0, top_k=100000, top_p=0.5)]
+    out, ref, gk, gp = run_both(fs, x, params, rng.random(rows), None)
+    assert (out["status"] & _lib.FIE_ROW_EXACT_PATH).any()
+    check(out, ref, params, gk, gp, lp=True)
+
+
+def test_ties_and_constant_rows(fs):
+    rows, vocab = 6, 40000
+    x = torch.zeros(rows, vocab)
+    x[1] = torch.arange(vocab) % 3            # three values, huge tie classes
+    x[2, 500:600] = 4.0
+    x[3] = -1.0
+    x[4, ::2] = 2.0
+    x[5] = float("-inf")
+    x[5, 777] = 1.0
+    params = [SamplingParams(temperature=1.0, top_p=0.5), SamplingParams(temperature=1.0, top_k=10),
+              SamplingParams(temperature=0.5, top_k=50, top_p=0.3, logprobs=20),
+              SamplingParams(temperature=1.0, top_p=0.01, logprobs=4),
+              SamplingParams(temperature=1.0, top_k=7, top_p=0.9),
+              SamplingParams(temperature=1.0, top_p=0.9, logprobs=2)]
+    out, ref, gk, gp = run_both(fs, x, params, np.linspace(0.01, 0.99, rows), None)
+    check(out, ref, params, gk, gp, lp=True)
+
+
+def test_long_history_counts_in_32_bits(fs):
+    rng = np.random.default_rng(3)
+    rows, vocab = 3, 50000
+    x = torch.from_numpy(rng.normal(0, 2.0, (rows, vocab)).astype(np.float32))
+    ctx = [[5] * 70000 + [0] * 3, list(rng.integers(0, vocab, 100)), [1, 2, 3]]
+    params = [SamplingParams(temperature=1.0, top_k=20, frequency_penalty=0.001),
+              SamplingParams(frequency_penalty=0.5, presence_penalty=0.1),
+              SamplingParams(temperature=0.9, top_p=0.8, repetition_penalty=1.9)]
+    out, ref, gk, gp = run_both(fs, x, params, rng.random(rows), ctx)
+    check(out, ref, params, gk, gp)
+
+
+def test_token0_penalty_quirk(fs):
+    """Q1: a penalised token 0 keeps its penalty only in the batch's widest row, and
+    an id >= vocab first seen after it undoes it (sampler.py:148,156-157,174-175)."""
+    vocab = 1000
+    x = torch.full((4, vocab), -3.0)
+    x[:, 0] = 5.0
+    x[:, 1] = 4.9
+    p = SamplingParams(repetition_penalty=2.0)
+    ctx = [[0, 7, 8, 9],          # widest row: token 0 penalised -> token 1 wins
+           [0],                   # narrower row: pad writes undo it -> token 0 wins
+           [7, 0, 8, vocab + 1],  # widest, but an invalid id after token 0 undoes it
+           [vocab + 1, 0, 7, 8]]  # widest, invalid id before token 0: penalty holds
+    out, ref, gk, gp = run_both(fs, x, [p] * 4, np.zeros(4), ctx)
+    check(out, ref, [p] * 4, gk, gp)
+    assert out["tokens"].tolist() == [1, 0, 0, 1]
+
+
+def test_repeated_launch_with_same_args(fs):
+    """The same argument block launched twice gives the same tokens (no state carried
+    between calls)."""
+    w = W.make(3, rows=SUBSETS[3])
+    hp = resolve_params(w.params, w.logits.shape[1], w.uniforms, w.contexts)
+    out, args, buf = fs.step(w.logits.to(DEV), hp)
+    first = out["tokens"].copy()
+    fs.launch(args)
+    buf.download(torch.cuda.current_stream())
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(buf.outputs()["tokens"], first)
+    ref = O.canonical_step(w.logits.float().numpy(), O.resolve(w.params, w.logits.shape[1]),
+                           w.uniforms, contexts=w.contexts)
+    np.testing.assert_array_equal(first, ref.tokens)
+
+
+def test_batched_sampler_end_to_end_logprobs(fs):
+    rng = np.random.default_rng(9)
+    rows, vocab = 10, 151936
+    x = torch.from_numpy(rng.normal(0, 3.0, (rows, vocab)).astype(np.float32)).half().to(DEV)
+    params = [SamplingParams(temperature=0.8, top_p=0.9, logprobs=5, seed=100 + r,
+                             presence_penalty=0.5) for r in range(rows)]
+    ctx = [list(rng.integers(0, vocab, 50)) for _ in range(rows)]
+    s = BatchedSampler(DEV)
+    res = s.sample(x, params, ctx, request_ids=[f"r{r}" for r in range(rows)])
+    assert len(res.token_ids) == rows and set(res.logprobs) == set(range(rows))
+    work = O.canonical_penalize(x.float().cpu().numpy(), O.resolve(params, vocab), ctx) / np.float32(0.8)
+    for r in range(rows):
+        lsm = O.log_softmax_ref(work[r])
+        entries = res.logprobs[r]
+        assert entries[0][0] == res.token_ids[r]
+        for tok, val in entries:
+            assert abs(val - lsm[tok]) <= 1e-5 * max(1.0, abs(lsm[tok])), (r, tok, val, lsm[tok])
+        alts = [t for t, _ in entries[1:]]
+        best = [int(i) for i in np.argsort(-lsm, kind="stable")[:5] if int(i) != res.token_ids[r]]
+        assert alts == best[:len(alts)]
+
+
+def test_batched_sampler_greedy_fast_path(fs):
+    x = torch.randn(33, 151936).half().to(DEV)
+    res = BatchedSampler(DEV).sample(x, [SamplingParams()] * 33)
+    assert res.token_ids == x.float().argmax(dim=-1).tolist()
+    assert res.logprobs == {}
+
+
+def test_seeded_rows_are_batch_independent(fs):
+    x = torch.randn(3, 5000).to(DEV)
+    p = [SamplingParams(temperature=1.0, seed=1234)] * 3
+    alone = BatchedSampler(DEV).sample(x[:1], p[:1]).token_ids[0]
+    with_others = BatchedSampler(DEV).sample(x, p).token_ids[0]
+    assert alone == with_others
+
+
+def test_c_abi_direct_calls_and_errors(fs):
+    lib = _lib.load()
+    ws = fs.ensure_workspace(4, 1000)
+    a = _lib.SamplerArgs()
+    assert lib.fie_sampler_sample(ctypes.byref(a), ctypes.byref(ws), None) == _lib.FIE_E_ARG
+    x = torch.randn(4, 1000, device=DEV)
+    out = torch.empty(4, dtype=torch.int64, device=DEV)
+    rc = lib.fie_sampler_argmax(x.data_ptr(), _lib.FIE_F32, 4, 1000, 1000, out.data_ptr(),
+                                ctypes.byref(ws), None)
+    assert rc == _lib.FIE_OK
+    torch.cuda.synchronize()
+    assert out.tolist() == x.argmax(-1).tolist()
+    small = _lib.Workspace(ws.ptr, 16, 4, 1000)
+    rc = lib.fie_sampler_argmax(x.data_ptr(), _lib.FIE_F32, 4, 1000, 1000, out.data_ptr(),
+                                ctypes.byref(small), None)
+    assert rc == _lib.FIE_E_WORKSPACE
+    rc = lib.fie_sampler_argmax(x.data_ptr(), 7, 4, 1000, 1000, out.data_ptr(), ctypes.byref(ws), None)
+    assert rc == _lib.FIE_E_ARG
+
+
+def test_cexp_matches_oracle(fs):
+    d = torch.linspace(-90.0, 0.0, 200001)
+    got = fs.cexp(d.to(DEV)).cpu().numpy()
+    want = O.cexp(d.numpy()[::97])
+    np.testing.assert_array_equal(got[::97].view(np.uint32), want.view(np.uint32))
