@@ -1,13 +1,16 @@
 """Benchmark of the fused MI355X sampler on the BASELINE workload (C3 by default).
 
-One step = one fused sampler call (penalties, temperature, filters, draw) over a
-[256, 151936] fp16 logits batch already resident in HBM, with the step's
-parameters and penalty histories resident too.  Logits rotate through enough
-distinct buffers (> 512 MB) that the 256 MB Infinity Cache cannot serve them.
+One step = one fused sampler call (penalties, temperature, top-k / top-p / min-p,
+draw, logprobs) over one [B, V] logits batch already resident in HBM, with the
+step's parameters and penalty histories resident too: the two kernels k_scan and
+k_finish.  Logits rotate through enough distinct buffers (> 512 MB) that the 256 MB
+Infinity Cache cannot serve them.
 
-Prints one JSON line: rows/s, us/step, the roofline of the dominant kernel (HIP
-events around each kernel of the chain), and the reference algorithm timed on
-this host's CPU (the torch-CPU restatement in oracle/, on a bounded sample).
+Prints one JSON line: rows/s and us/step for the headline config, the roofline of
+the dominant kernel (HIP events on the launch stream around each kernel), the other
+configs' times, the end-to-end BatchedSampler.sample() time (host packing, upload,
+kernels, download), and the reference algorithm timed on this host's CPU (the
+torch-CPU restatement in oracle/, on a bounded sample of rows).
 """
 
 from __future__ import annotations
@@ -16,6 +19,7 @@ import argparse
 import json
 import math
 import os
+import platform
 import statistics
 import sys
 import time
@@ -25,7 +29,7 @@ sys.path.insert(0, os.path.join(_REPO, "full-inference-engine_amd"))
 
 METRIC = "rows/s + µs per sampler step at B=256,V=152k; % of HBM roofline"
 HBM_PEAK_GBS = 8000.0
-STAGES = ("k_penalty", "k_sample")
+STAGES = ("k_scan", "k_finish")
 
 
 def parse():
@@ -33,158 +37,246 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--config", type=int, default=3, help="workload C1..C5 (default C3)")
+    ap.add_argument("--config", type=int, default=3, help="headline workload C1..C5 (default C3)")
+    ap.add_argument("--others", default="1,2,4,5", help="other configs to time ('' for none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=64)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--ring-mb", type=int, default=640)
     return ap.parse_args()
 
 
-def main() -> None:
-    a = parse()
-    if a.gpus != 1:
-        print(json.dumps({"error": "this build measures one GPU: rows are independent and "
-                          "every GPU box has one GPU; run with --gpus 1"}))
-        sys.exit(2)
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def algorithmic_bytes(w, hp) -> dict:
+    """Bytes one step must move at least (one read of the logits), per kernel.
+
+    k_scan: the logits once, each penalised row's history ids once, per-row params;
+            its outputs (tile partials) are counted too.
+    step:   the logits once, the history once, per-row params in and results out
+            (48 bytes per row), as BASELINE.md's table counts them.
+    """
+    B, V = w.logits.shape
+    esize = w.logits.element_size()
+    hist = 4 * int(hp.hist_off[-1]) if hp.apply_penalties else 0
+    logits = B * V * esize
+    return {"logits": logits, "history": hist,
+            "k_scan": logits + hist + 48 * B,
+            "step": logits + hist + 48 * B}
+
+
+def time_config(config: int, steps: int, warmup: int, ring_mb: int, dev):
     import numpy as np
     import torch
 
+    from fie_amd import _lib
     from fie_amd import workloads as W
     from fie_amd.batching.sampler import resolve_params
     from fie_amd.kernel import FusedSampler
 
-    dev = torch.device("cuda:0")
-    w = W.make(a.config, device=dev)
+    w = W.make(config, device=dev)
     B, V = w.logits.shape
-    esize = w.logits.element_size()
     hp = resolve_params(w.params, V, w.uniforms, w.contexts)
-    hist_total = int(hp.hist_off[-1]) if hp.apply_penalties else 0
     fs = FusedSampler(dev)
+    hist_total = int(hp.hist_off[-1]) if hp.apply_penalties else 0
     buf = fs.step_buffers(B, hist_total)
     buf.stage(hp)
     stream = torch.cuda.current_stream(dev)
     buf.upload(stream)
-
-    logits_bytes = B * V * esize
-    nbuf = max(2, math.ceil(a.ring_mb * 2**20 / logits_bytes))
+    logits_bytes = w.logits.numel() * w.logits.element_size()
+    nbuf = max(2, math.ceil(ring_mb * 2**20 / logits_bytes))
     ring = [w.logits] + [w.logits.clone() for _ in range(nbuf - 1)]
-    args = [fs.build_args(x, buf, hp.apply_penalties, hist_total) for x in ring]
-    fs.ensure_workspace(B, V, hist_total)
+    args = [fs.build_args(x, buf, hp) for x in ring]
+    fs.ensure_workspace(B, V)
     torch.cuda.synchronize()
 
-    def one_step(i):
-        fs.launch(args[i % nbuf], hist_total)
-
-    for i in range(a.warmup):
-        one_step(i)
+    for i in range(warmup):
+        fs.launch(args[i % nbuf])
     torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record(stream)
-    for i in range(a.steps):
-        one_step(i)
-    end.record(stream)
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(steps):
+        fs.launch(args[i % nbuf])
+    t1.record(stream)
     torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(end) / a.steps
+    ms_per_step = t0.elapsed_time(t1) / steps
 
-    # Per-kernel durations: the same steps, one HIP event between kernels.
+    # Per-kernel durations: the same launches, one HIP event between kernels, all on
+    # the stream the kernels run on.
     nst = len(STAGES)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(nst + 1)] for _ in range(a.steps)]
-    for i in range(a.steps):
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(nst + 1)] for _ in range(steps)]
+    for i in range(steps):
         ev[i][0].record(stream)
         for s in range(nst):
-            fs.launch_stage(args[i % nbuf], hist_total, s)
+            fs.launch_stage(args[i % nbuf], s)
             ev[i][s + 1].record(stream)
     torch.cuda.synchronize()
-    stage_ms = [statistics.mean(ev[i][s].elapsed_time(ev[i][s + 1]) for i in range(a.steps))
+    stage_ms = [statistics.median(ev[i][s].elapsed_time(ev[i][s + 1]) for i in range(steps))
                 for s in range(nst)]
 
-    # One checked step: every row resolved on the fast path.
+    # One checked step: status bits of the rows (the exact path is informational).
     buf.download(stream)
     torch.cuda.synchronize()
     out = buf.outputs()
-    overflow_rows = int((out["status"] & 1 != 0).sum())
-    timeout_rows = int((out["status"] & 2 != 0).sum())
-
-    # Algorithmic bytes: logits once, penalty histories, per-row params/uniform/out.
-    step_bytes = logits_bytes + 4 * hist_total + 48 * B
-    # k_penalty: history ids in, one logit gathered and an (id, value) pair out per id;
-    # k_sample: the logits once, the penalty pairs, per-row params and outputs.
-    stage_bytes = [4 * hist_total + 2 * hist_total + 8 * hist_total,
-                   logits_bytes + 8 * hist_total + 48 * B]
-    dom = max(range(nst), key=lambda s: stage_ms[s])
-    achieved = stage_bytes[dom] / (stage_ms[dom] * 1e-3) / 1e9
-    step_gbs = step_bytes / (ms_per_step * 1e-3) / 1e9
-
-    line = {
-        "metric": METRIC,
-        "value": B / (ms_per_step * 1e-3),
-        "unit": "rows/s",
-        "n_gpus": 1,
-        "steps": a.steps,
-        "warmup": a.warmup,
-        "ms_per_step": ms_per_step,
-        "us_per_step": ms_per_step * 1e3,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic",
-        "config": {
-            "workload": f"{w.name}: B={B}, V={V}, {str(w.logits.dtype).replace('torch.', '')} "
-                        "logits, seeded synthetic (fie_amd/workloads.py)",
-            "rows": B, "vocab": V, "logits_dtype": str(w.logits.dtype).replace("torch.", ""),
-            "history_ids": hist_total, "logits_ring_buffers": nbuf,
-        },
-        "roofline": {
-            "bound": "hbm",
-            "kernel": STAGES[dom],
-            "achieved": achieved,
-            "peak": HBM_PEAK_GBS,
-            "unit": "GB/s",
-            "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
-        },
-        "step_roofline": {"achieved": step_gbs, "frac": step_gbs / HBM_PEAK_GBS,
-                          "algorithmic_bytes": step_bytes},
-        "stage_us": {STAGES[s]: stage_ms[s] * 1e3 for s in range(nst)},
-        "overflow_rows": overflow_rows,
-        "timeout_rows": timeout_rows,
+    exact_rows = int((out["status"] & _lib.FIE_ROW_EXACT_PATH != 0).sum())
+    return {
+        "w": w, "hp": hp, "B": B, "V": V, "ms_per_step": ms_per_step,
+        "stage_ms": dict(zip(STAGES, stage_ms)), "exact_path_rows": exact_rows,
+        "ring": nbuf, "bytes": algorithmic_bytes(w, hp), "fs": fs,
     }
-    if not a.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline(w, a.cpu_rows)
-    print(json.dumps(line), flush=True)
 
 
-def cpu_baseline(w, rows: int) -> dict:
-    """The reference algorithm (torch-CPU restatement, oracle/oracle.py) on a sample
-    of the same workload: `rows` rows spread evenly over the batch, same params."""
+def end_to_end_ms(w, dev, reps: int = 20) -> float:
+    """BatchedSampler.sample() as the engine calls it: parameter packing, history
+    packing, upload, the kernels, download and the host lists, per call."""
+    import torch
+
+    from fie_amd.batching.sampler import BatchedSampler
+
+    s = BatchedSampler(dev, generator_seed=0)
+    x = w.logits
+    ids = [f"r{i}" for i in range(x.shape[0])]
+    s.sample(x, w.params, w.contexts, ids)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        t = time.perf_counter()
+        s.sample(x, w.params, w.contexts, ids)
+        times.append(time.perf_counter() - t)
+    return statistics.median(times) * 1e3
+
+
+def cpu_baseline(w, seconds: float) -> dict:
+    """The reference algorithm (torch-CPU restatement, oracle/oracle.py) on a sample of
+    the same workload: rows spread evenly over the batch, same params and histories,
+    as many rows as fit about `seconds` of CPU work."""
     import numpy as np
     import torch
 
     sys.path.insert(0, os.path.join(_REPO, "oracle"))
     import oracle as O
 
-    B = w.logits.shape[0]
-    rows = min(rows, B)
-    idx = np.linspace(0, B - 1, rows).round().astype(int).tolist()
-    logits = w.logits[torch.tensor(idx, device=w.logits.device)].cpu()
-    params = [w.params[i] for i in idx]
-    ctx = [w.contexts[i] for i in idx] if w.contexts is not None else None
-    uni = w.uniforms[idx]
-    threads = min(os.cpu_count() or 1, 16)
+    threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    O.torch_reference_step(logits, params, ctx, uni)          # warm-up
+    B = w.logits.shape[0]
+
+    def sample(rows):
+        idx = np.linspace(0, B - 1, rows).round().astype(int).tolist()
+        logits = w.logits[torch.tensor(idx, device=w.logits.device)].cpu()
+        params = [w.params[i] for i in idx]
+        ctx = [w.contexts[i] for i in idx] if w.contexts is not None else None
+        return logits, params, ctx, w.uniforms[idx]
+
+    probe = sample(min(8, B))
+    t = time.perf_counter()
+    O.torch_reference_step(*probe)
+    per_row = (time.perf_counter() - t) / probe[0].shape[0]
+    rows = int(max(8, min(B, seconds / 4 / max(per_row, 1e-6))))
+    data = sample(rows)
+    O.torch_reference_step(*data)                        # warm-up
     times = []
-    budget = time.perf_counter() + 20.0
+    budget = time.perf_counter() + seconds
     while len(times) < 3 or (time.perf_counter() < budget and len(times) < 10):
-        t0 = time.perf_counter()
-        O.torch_reference_step(logits, params, ctx, uni)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times)
-    return {"value": rows / t, "unit": "rows/s", "cores": threads, "kind": "port",
-            "sample": f"{rows} of {B} rows of {w.name} (same params and histories), "
-                      f"median of {len(times)} steps, {t * 1e3:.1f} ms/step, torch "
-                      f"{torch.__version__} CPU, {threads} threads"}
+        t = time.perf_counter()
+        O.torch_reference_step(*data)
+        times.append(time.perf_counter() - t)
+    med = statistics.median(times)
+    return {"value": rows / med, "unit": "rows/s", "cores": threads, "kind": "port",
+            "sample": f"{rows} of {B} rows of {w.name} (same params and histories), median of "
+                      f"{len(times)} steps, {med * 1e3:.1f} ms/step; torch {torch.__version__} CPU, "
+                      f"{threads} threads on {cpu_model()}"}
+
+
+def main() -> None:
+    a = parse()
+    if a.gpus != 1:
+        print(json.dumps({"error": "this build measures one GPU (every GPU box here has one); "
+                          "rows are independent, so more GPUs shard rows without "
+                          "communication; run with --gpus 1"}))
+        sys.exit(2)
+    import torch
+
+    dev = torch.device("cuda:0")
+    main_r = time_config(a.config, a.steps, a.warmup, a.ring_mb, dev)
+    w = main_r["w"]
+    B, V = main_r["B"], main_r["V"]
+    ms = main_r["ms_per_step"]
+    st = main_r["stage_ms"]
+    dom = max(STAGES, key=lambda s: st[s])
+    by = main_r["bytes"]
+    dom_bytes = by[dom] if dom in by else by["step"]
+    achieved = dom_bytes / (st[dom] * 1e-3) / 1e9
+    step_gbs = by["step"] / (ms * 1e-3) / 1e9
+    ldt = str(w.logits.dtype).replace("torch.", "")
+
+    line = {
+        "metric": METRIC,
+        "value": B / (ms * 1e-3),
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": ms,
+        "us_per_step": ms * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": f"{ldt} logits, f32 arithmetic, exact integer masses",
+        "data": "synthetic, seeded (fie_amd/workloads.py)",
+        "config": {
+            "workload": f"{w.name}: B={B}, V={V}, {ldt} logits, mixed per-row greedy/top-k/"
+                        "top-p/penalties" if a.config == 3 else f"{w.name}: B={B}, V={V}, {ldt}",
+            "rows": B, "vocab": V, "logits_dtype": ldt,
+            "history_ids": int(main_r["hp"].hist_off[-1]) if main_r["hp"].apply_penalties else 0,
+            "logits_ring_buffers": main_r["ring"],
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom,
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "algorithmic_bytes": dom_bytes,
+        },
+        "step_roofline": {"achieved": step_gbs, "frac": step_gbs / HBM_PEAK_GBS,
+                          "algorithmic_bytes": by["step"]},
+        "stage_us": {k: v * 1e3 for k, v in st.items()},
+        "exact_path_rows": main_r["exact_path_rows"],
+    }
+    del main_r
+    others = {}
+    for c in [int(x) for x in a.others.split(",") if x.strip()]:
+        if c == a.config:
+            continue
+        r = time_config(c, max(20, a.steps // 4), 5, a.ring_mb, dev)
+        gbs = r["bytes"]["step"] / (r["ms_per_step"] * 1e-3) / 1e9
+        others[f"C{c}"] = {"rows": r["B"], "vocab": r["V"],
+                           "dtype": str(r["w"].logits.dtype).replace("torch.", ""),
+                           "us_per_step": r["ms_per_step"] * 1e3,
+                           "rows_per_s": r["B"] / (r["ms_per_step"] * 1e-3),
+                           "stage_us": {k: v * 1e3 for k, v in r["stage_ms"].items()},
+                           "step_frac_hbm": gbs / HBM_PEAK_GBS,
+                           "exact_path_rows": r["exact_path_rows"]}
+        del r
+        torch.cuda.empty_cache()
+    line["other_configs"] = others
+    try:
+        line["end_to_end_ms"] = end_to_end_ms(w, dev)
+    except Exception as e:  # report, never hide the main line
+        line["end_to_end_ms"] = f"failed: {e}"
+    if not a.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(w, a.cpu_seconds)
+    print(json.dumps(line), flush=True)
 
 
 if __name__ == "__main__":

@@ -15,7 +15,7 @@ typedef unsigned __int128 u128;
 // Tokens per tile.  Part of the canonical weight rule: a token's weight is taken
 // relative to the largest scaled logit of its tile (token 0 is a tile of its own,
 // then [1, kTile), [kTile, 2 kTile), ...).
-constexpr int kTile = 8192;
+constexpr int kTile = 2048;
 
 // ---------------------------------------------------------------- order keys
 // Order-preserving key of an fp32 value: larger value -> larger key.  Callers fold
@@ -50,16 +50,21 @@ FIE_DEV uint32_t comp_k(uint64_t c) { return (uint32_t)(c >> 32); }
 FIE_DEV float scaled(float w, float s) { return w / s + 0.0f; }
 
 // ---------------------------------------------------------------- exponential
-// Canonical fp32 exponential of d <= 0: Cody-Waite reduction by a two-part ln 2,
-// degree-7 Taylor polynomial on |r| <= ln2/2 by Horner with fused multiply-adds,
-// exact scaling by 2^n.  Each step is one IEEE binary32 operation, so any
+// Canonical fp32 exponential of d <= 0: 0 for d <= -80 (and -inf, NaN), 1 for
+// d >= 0, otherwise Cody-Waite reduction by a two-part ln 2, a degree-7 Taylor
+// polynomial on |r| <= ln2/2 by Horner with fused multiply-adds, and an exact
+// scaling by 2^n.  Each step is one IEEE binary32 operation, so any
 // implementation performing the same steps returns the same bits.
-FIE_DEV float cexp(float d)
+//
+// cexp_scaled(d, extra) is cexp(d) * 2^extra, computed without branches: the
+// polynomial runs on max(d, -80) and the two special cases are selected after.
+// The final ldexp is exact for the small `extra` used here because cexp(d) >=
+// 2^-116 stays normal on (-80, 0).
+FIE_DEV float cexp_scaled(float d, int extra)
 {
-    if (!(d > -80.0f)) return 0.0f;
-    if (d >= 0.0f) return 1.0f;
-    float n = __builtin_rintf(d * 1.44269502f);
-    float r = __builtin_fmaf(n, -0.693145752f, d);
+    const float dc = __builtin_fmaxf(d, -80.0f);
+    const float n = __builtin_rintf(dc * 1.44269502f);
+    float r = __builtin_fmaf(n, -0.693145752f, dc);
     r = __builtin_fmaf(n, -1.42860677e-06f, r);
     float p = 1.98412701e-04f;
     p = __builtin_fmaf(p, r, 1.38888892e-03f);
@@ -69,8 +74,12 @@ FIE_DEV float cexp(float d)
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return __builtin_ldexpf(p, (int)n);
+    const float v = __builtin_ldexpf(p, (int)n + extra);
+    const float one = __builtin_ldexpf(1.0f, extra);
+    return (d > -80.0f) ? ((d >= 0.0f) ? one : v) : 0.0f;
 }
+
+FIE_DEV float cexp(float d) { return cexp_scaled(d, 0); }
 
 // floor(e * 2^40) of e in [0, 1].  e * 2^40 is exact in double, so the conversion
 // only truncates.
@@ -231,6 +240,81 @@ FIE_DEV u128 wave_incl_scan_u128(u128 v)
         if (lane >= d) v += o;
     }
     return v;
+}
+
+// ---------------------------------------------------------------- DPP wave helpers
+// Cross-lane steps by data-parallel primitives (no LDS round trip).  After the four
+// steps inside a row of 16 lanes every lane of the row holds the row's result; the
+// four row results are then combined from lanes 0, 16, 32, 48 in scalar registers.
+template <int CTRL>
+FIE_DEV uint32_t dpp_mov(uint32_t v)
+{
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+
+FIE_DEV uint32_t rl(uint32_t v, int lane) { return (uint32_t)__builtin_amdgcn_readlane((int)v, lane); }
+
+FIE_DEV uint32_t dwave_max_u32(uint32_t v)
+{
+    v = max(v, dpp_mov<kDppXor1>(v));
+    v = max(v, dpp_mov<kDppXor2>(v));
+    v = max(v, dpp_mov<kDppHalfMirror>(v));
+    v = max(v, dpp_mov<kDppMirror>(v));
+    return max(max(rl(v, 0), rl(v, 16)), max(rl(v, 32), rl(v, 48)));
+}
+
+FIE_DEV uint32_t dwave_min_u32(uint32_t v)
+{
+    v = min(v, dpp_mov<kDppXor1>(v));
+    v = min(v, dpp_mov<kDppXor2>(v));
+    v = min(v, dpp_mov<kDppHalfMirror>(v));
+    v = min(v, dpp_mov<kDppMirror>(v));
+    return min(min(rl(v, 0), rl(v, 16)), min(rl(v, 32), rl(v, 48)));
+}
+
+FIE_DEV uint64_t dwave_sum_u64(uint64_t v)
+{
+    auto step = [](uint64_t x, auto mv) {
+        const uint32_t lo = mv((uint32_t)x), hi = mv((uint32_t)(x >> 32));
+        return x + (((uint64_t)hi << 32) | lo);
+    };
+    v = step(v, [](uint32_t a) { return dpp_mov<kDppXor1>(a); });
+    v = step(v, [](uint32_t a) { return dpp_mov<kDppXor2>(a); });
+    v = step(v, [](uint32_t a) { return dpp_mov<kDppHalfMirror>(a); });
+    v = step(v, [](uint32_t a) { return dpp_mov<kDppMirror>(a); });
+    uint64_t t = 0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+        t += ((uint64_t)rl((uint32_t)(v >> 32), 16 * r) << 32) | rl((uint32_t)v, 16 * r);
+    return t;
+}
+
+// Exclusive prefix sum over the lanes of a wave (lane 0 first), and the total.
+FIE_DEV uint32_t dwave_excl_scan_u32(uint32_t v, uint32_t* total)
+{
+    const int lane = threadIdx.x & 63;
+    uint32_t x = v;
+    // inclusive scan inside each row of 16: shifts by 1, 2, 4, 8 (0 shifted in)
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x111, 0xF, 0xF, true);
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x112, 0xF, 0xF, true);
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x114, 0xF, 0xF, true);
+    x += (uint32_t)__builtin_amdgcn_update_dpp(0, (int)x, 0x118, 0xF, 0xF, true);
+    const uint32_t r0 = rl(x, 15), r1 = rl(x, 31), r2 = rl(x, 47), r3 = rl(x, 63);
+    const int row = lane >> 4;
+    const uint32_t before = (row > 0 ? r0 : 0u) + (row > 1 ? r1 : 0u) + (row > 2 ? r2 : 0u);
+    *total = r0 + r1 + r2 + r3;
+    return before + x - v;
+}
+
+FIE_DEV uint32_t popc64(uint64_t m) { return (uint32_t)__builtin_popcountll(m); }
+
+// Orders this wave's earlier LDS writes before its later LDS reads (other lanes'
+// writes included) without a workgroup barrier.
+FIE_DEV void wave_lds_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
 }
 
 // ---------------------------------------------------------------- block helpers

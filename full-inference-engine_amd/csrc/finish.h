@@ -14,8 +14,9 @@
 namespace fie {
 
 constexpr int kFinThreads = 512;
-constexpr int kGCap = 8192;        // composites held in LDS (candidates / a gathered bin)
+constexpr int kGCap = 8192 + 64;   // composites held in LDS (candidates / a gathered bin)
 constexpr int kPassBins = 2048;    // bins of a full-row radix pass
+constexpr int kChunk = 8192;       // tokens per step of a full-row pass
 
 // Radix digits over the 64-bit rank composite (key << 32 | ~index): three over the
 // key, then three over the index (bits 31..24 of ~index are constant for V < 2^24).
@@ -35,7 +36,7 @@ struct FinSmem {
     uint64_t cand[kGCap];                       // candidates or a gathered key range
     uint32_t pc[kPassBins];                     // full-row pass: counts per bin
     uint64_t pm_lo[kPassBins], pm_hi[kPassBins];// full-row pass: mass per bin
-    uint32_t cnt[kTile];                        // penalty counts of one tile
+    uint32_t cnt[kChunk];                       // penalty counts of one chunk
     uint32_t hc[256];                           // LDS selection: counts per digit
     uint64_t hm_lo[256], hm_hi[256];            // LDS selection: mass per digit
     float mt[kMaxTiles + 1];                    // tile maxima of y (slot 0 = token 0)
@@ -84,11 +85,11 @@ struct Pred {
 template <bool MASS>
 FIE_DEV SelResult lds_select(FinSmem& S, int n, const Pred pr, u128 g)
 {
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     uint64_t prefix = 0, pmask = 0;
     u128 excl = 0;
     for (int level = 0; level < 64; ++level) {
-        // range of the remaining elements
+        // range of the remaining elements (one barrier), and a cleared histogram
         uint64_t mn = ~0ull, mx = 0;
         for (int i = tid; i < n; i += kFinThreads) {
             const uint64_t c = S.cand[i];
@@ -97,33 +98,42 @@ FIE_DEV SelResult lds_select(FinSmem& S, int n, const Pred pr, u128 g)
                 mx = c > mx ? c : mx;
             }
         }
-        mx = block_max_u64<kFinThreads>(mx, S.red64);
-        mn = ~block_max_u64<kFinThreads>(~mn, S.red64);
-        if (mx == 0 && mn == ~0ull) return SelResult{0, 0, 0, 0};
-        if (mn == mx) {
+        for (int i = tid; i < 256; i += kFinThreads) {
+            S.hc[i] = 0;
+            if (MASS) { S.hm_lo[i] = 0; S.hm_hi[i] = 0; }
+        }
+        mx = wave_max_u64(mx);
+        mn = ~wave_max_u64(~mn);
+        if (lane == 0) { S.red64[wave] = mx; S.red64[8 + wave] = mn; }
+        __syncthreads();
+        mx = 0;
+        mn = ~0ull;
+#pragma unroll
+        for (int w = 0; w < kFinThreads / 64; ++w) {
+            mx = S.red64[w] > mx ? S.red64[w] : mx;
+            mn = S.red64[8 + w] < mn ? S.red64[8 + w] : mn;
+        }
+        if (mn >= mx) {
+            __syncthreads();   // S.red64 is read above: no thread may reuse it yet
+            if (mx == 0) return SelResult{0, 0, 0, 0};
             const u128 m = MASS ? comp_weight(S, mx) : (u128)1;
             return SelResult{mx, excl, m, g < m ? 1 : 0};
         }
         const int hb = 63 - __builtin_clzll(mn ^ mx);
         const int shift = hb >= 7 ? hb - 7 : 0;
-        for (int i = tid; i < 256; i += kFinThreads) {
-            S.hc[i] = 0;
-            if (MASS) { S.hm_lo[i] = 0; S.hm_hi[i] = 0; }
-        }
-        __syncthreads();
         const uint64_t hmask = (hb >= 63) ? 0ull : ~((2ull << hb) - 1);
         for (int i = tid; i < n; i += kFinThreads) {
             const uint64_t c = S.cand[i];
-            if ((c & hmask) == (mn & hmask) && (c & pmask) == prefix && pr(c)) {
+            if ((c & pmask) == prefix && pr(c)) {
                 const int d = (int)((c >> shift) & 0xFFu);
-                atomicAdd(&S.hc[d], 1u);
                 if (MASS) {
                     const u128 w = comp_weight(S, c);
                     const uint64_t lo = (uint64_t)w;
                     const uint64_t old = atomicAdd((unsigned long long*)&S.hm_lo[d], (unsigned long long)lo);
-                    const uint64_t carry = (old + lo < old) ? 1ull : 0ull;
-                    const uint64_t hi = (uint64_t)(w >> 64) + carry;
+                    const uint64_t hi = (uint64_t)(w >> 64) + ((old + lo < old) ? 1ull : 0ull);
                     if (hi) atomicAdd((unsigned long long*)&S.hm_hi[d], (unsigned long long)hi);
+                } else {
+                    atomicAdd(&S.hc[d], 1u);
                 }
             }
         }
@@ -155,22 +165,23 @@ FIE_DEV SelResult lds_select(FinSmem& S, int n, const Pred pr, u128 g)
         __syncthreads();
         const int d = S.ibin;
         const u128 above = S.bex;
-        __syncthreads();
-        if (d < 0) return SelResult{0, excl + above, 0, 0};
+        if (d < 0) {
+            __syncthreads();
+            return SelResult{0, excl + above, 0, 0};
+        }
         g -= above;
         excl += above;
         prefix = (mn & hmask) | ((uint64_t)d << shift);
-        pmask = ~((1ull << shift) - 1) | hmask;
-        if (shift == 0) pmask = ~0ull;
+        pmask = shift == 0 ? ~0ull : (~((1ull << shift) - 1) | hmask);
     }
     return SelResult{0, 0, 0, 0};
 }
 
 // ---------------------------------------------------------------- full-row passes
-// Penalty counts of tile [lo, hi) of `row` into S.cnt (one u32 per token).
+// Penalty counts of tokens [lo, hi) of `row` into S.cnt (one u32 per token).
 FIE_DEV void recount(FinSmem& S, const fie_sampler_args& a, int row, int lo, int hi)
 {
-    for (int i = threadIdx.x; i < kTile; i += kFinThreads) S.cnt[i] = 0;
+    for (int i = threadIdx.x; i < kChunk; i += kFinThreads) S.cnt[i] = 0;
     __syncthreads();
     const int64_t h0 = a.hist_offsets[row], h1 = a.hist_offsets[row + 1];
     for (int64_t h = h0 + threadIdx.x; h < h1; h += kFinThreads) {
@@ -189,13 +200,13 @@ FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, 
                       float pres, float freq, uint32_t k0, F&& f)
 {
     constexpr int EPL = DTy<DT>::EPL, SZ = DTy<DT>::SZ;
-    constexpr int NL = kTile / kFinThreads / EPL;
+    constexpr int NL = kChunk / kFinThreads / EPL;
     const fie_sampler_args& a = P.a;
     const int V = a.vocab, tid = threadIdx.x;
     const char* rowp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * SZ;
     if (tid == 0 && k0) f(comp_key(k0, 0));
-    for (int tile = 0; tile < P.NT; ++tile) {
-        const int lo = tile * kTile, hi = min(lo + kTile, V);
+    for (int lo = 0; lo < V; lo += kChunk) {
+        const int hi = min(lo + kChunk, V);
         uint4 raw[NL];
 #pragma unroll
         for (int j = 0; j < NL; ++j) raw[j] = load_group<DT, VEC>(rowp, lo + (j * kFinThreads + tid) * EPL, V);
@@ -393,6 +404,25 @@ FIE_DEV bool q1_keeps(FinSmem& S, const KParams& P, int row)
     return mine == wmax && !late;
 }
 
+// The row's candidates from every tile into S.cand as y-domain composites, token 0
+// last; one element per thread, all loads in flight together.
+FIE_DEV void load_candidates(FinSmem& S, const KParams& P, int row, int NT, int n, float s,
+                             uint32_t k0)
+{
+    for (int i = threadIdx.x; i < n - 1; i += kFinThreads) {
+        int lo = 0, hi = NT - 1;                 // tile t with coff[t] <= i < coff[t+1]
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (S.coff[mid] <= (uint32_t)i) lo = mid;
+            else hi = mid - 1;
+        }
+        const uint64_t xc = P.w.cand[((size_t)row * NT + lo) * kCapW + (i - S.coff[lo])];
+        S.cand[i] = comp_key(fkey(y_of_xkey(comp_k(xc), s)), comp_idx(xc));
+    }
+    if (threadIdx.x == 0) S.cand[n - 1] = comp_key(k0, 0);
+    __syncthreads();
+}
+
 // ---------------------------------------------------------------- k_finish
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
@@ -481,39 +511,23 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
     uint32_t safe = 0;
     const bool need_cand = !greedy || lp > 0;
     if (need_cand) {
-        if (tid == 0) {
-            uint32_t off = 0, kx = 0;
-            for (int t = 0; t < NT; ++t) {
-                S.coff[t] = off;
-                off += P.w.ncand[(size_t)row * NT + t];
-                const uint32_t b = P.w.bound[(size_t)row * NT + t];
-                kx = b > kx ? b : kx;
-            }
-            S.coff[NT] = off;
-            S.n = off + 1;
-            S.red32[0] = kx;
-        }
+        // per-tile counts and bounds: one load per thread, a block prefix sum
+        const uint32_t m = tid < NT ? P.w.ncand[(size_t)row * NT + tid] : 0u;
+        const uint32_t b = tid < NT ? P.w.bound[(size_t)row * NT + tid] : 0u;
+        uint32_t total;
+        const uint32_t off = block_excl_scan_u32<kFinThreads>(m, S.red32, &total);
+        if (tid < NT) S.coff[tid] = off;
+        const uint32_t kxm = block_max_u32<kFinThreads>(b, S.red32);
+        if (tid == 0) { S.coff[NT] = total; S.n = total + 1; S.red32[16] = kxm; }
         __syncthreads();
         n = (int)S.n;
-        const uint32_t kx = S.red32[0];
+        const uint32_t kx = S.red32[16];
         __syncthreads();
         if (kx <= 1u || kx <= kKeyNegInf) safe = 0;
         else if (kx > kKeyPosInf) safe = 0xFFFFFFFFu;
         else safe = fkey(y_of_xkey(kx, s));
-        if (n > kGCap) {
-            deep = true;
-        } else {
-            for (int t = 0; t < NT; ++t) {
-                const uint32_t o = S.coff[t], m = S.coff[t + 1] - o;
-                const uint64_t* src = P.w.cand + ((size_t)row * NT + t) * kCap;
-                for (uint32_t i = tid; i < m; i += kFinThreads) {
-                    const uint64_t xc = src[i];
-                    S.cand[o + i] = comp_key(fkey(y_of_xkey(comp_k(xc), s)), comp_idx(xc));
-                }
-            }
-            if (tid == 0) S.cand[n - 1] = comp_key(k0, 0);
-            __syncthreads();
-        }
+        if (n > kGCap) deep = true;
+        else load_candidates(S, P, row, NT, n, s, k0);
     }
 
     // Sampled rows on the candidates: top-k, min-p, S, top-p cut, draw.
@@ -606,16 +620,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
         token = comp_idx(tok_comp);
         if (a.tk_key && tid == 0) a.tk_key[row] = tk;
         // the LDS candidates were overwritten: reload them for the logprobs below
-        if (lp > 0 && n <= kGCap) {
-            for (int t = 0; t < NT; ++t) {
-                const uint32_t o = S.coff[t], m = S.coff[t + 1] - o;
-                const uint64_t* src = P.w.cand + ((size_t)row * NT + t) * kCap;
-                for (uint32_t i = tid; i < m; i += kFinThreads)
-                    S.cand[o + i] = comp_key(fkey(y_of_xkey(comp_k(src[i]), s)), comp_idx(src[i]));
-            }
-            if (tid == 0) S.cand[n - 1] = comp_key(k0, 0);
-            __syncthreads();
-        }
+        if (lp > 0 && n <= kGCap) load_candidates(S, P, row, NT, n, s, k0);
     }
 
     // Logprobs (sampler.py:262-291, rule R7): chosen token, then the row's best L,

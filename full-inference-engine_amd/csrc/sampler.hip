@@ -16,16 +16,18 @@
 namespace fie {
 
 // ---------------------------------------------------------------- greedy fast path
-// Tile maxima of the raw logits (token 0 included, no penalties, no scaling).
+constexpr int kArgChunk = 8192;   // tokens per workgroup of the argmax pass
+
+// Chunk maxima of the raw logits (token 0 included, no penalties, no scaling).
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kScanThreads) void k_argmax_scan(const void* logits, int V,
                                                               int64_t stride, int NT,
                                                               uint64_t* maxc)
 {
-    constexpr int EPL = DTy<DT>::EPL, SZ = DTy<DT>::SZ, NL = kEPT / EPL;
+    constexpr int EPL = DTy<DT>::EPL, SZ = DTy<DT>::SZ, NL = kArgChunk / kScanThreads / EPL;
     __shared__ uint32_t scr[32];
     const int tile = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
-    const int lo = tile * kTile;
+    const int lo = tile * kArgChunk;
     const char* rowp = (const char*)logits + (size_t)row * (size_t)stride * SZ;
     uint4 raw[NL];
 #pragma unroll
@@ -62,12 +64,12 @@ __global__ __launch_bounds__(64) void k_argmax_finish(const uint64_t* maxc, int 
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kScanThreads) void k_kept(const KParams P, uint8_t* kept, float* probs)
 {
-    constexpr int EPL = DTy<DT>::EPL, SZ = DTy<DT>::SZ, NL = kEPT / EPL;
-    __shared__ uint32_t cnt[kTile];
+    constexpr int EPL = DTy<DT>::EPL, SZ = DTy<DT>::SZ, NL = kArgChunk / kScanThreads / EPL;
+    __shared__ uint32_t cnt[kArgChunk];
     const fie_sampler_args& a = P.a;
-    const int tile = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int row = blockIdx.y, tid = threadIdx.x;
     const int NT = P.NT, V = a.vocab;
-    const int lo = tile * kTile, hi = min(lo + kTile, V);
+    const int lo = blockIdx.x * kArgChunk, hi = min(lo + kArgChunk, V);
     const RowRes rr = P.w.res[row];
     const bool pen = a.apply_penalties && (a.flags[row] & FIE_FLAG_PENALTY);
     const float* mt = P.w.mt + (size_t)row * (NT + 1);
@@ -79,7 +81,7 @@ __global__ __launch_bounds__(kScanThreads) void k_kept(const KParams P, uint8_t*
         rep = a.repetition[row];
         pres = a.presence[row];
         freq = a.frequency[row];
-        for (int i = tid; i < kTile; i += kScanThreads) cnt[i] = 0;
+        for (int i = tid; i < kArgChunk; i += kScanThreads) cnt[i] = 0;
         __syncthreads();
         const int64_t h0 = a.hist_offsets[row], h1 = a.hist_offsets[row + 1];
         for (int64_t h = h0 + tid; h < h1; h += kScanThreads) {
@@ -159,7 +161,7 @@ static bool layout_of(int32_t R, int32_t V, Layout* L)
     L->bound = take(r * NT * 4);
     L->ncand = take(r * NT * 4);
     L->nu = take(r * NT * 4);
-    L->cand = take(r * NT * kCap * 8);
+    L->cand = take(r * NT * kCapW * 8);
     L->tok0x = take(r * 4);
     L->tok0c = take(r * 4);
     L->bad = take(r * 4);
@@ -232,7 +234,7 @@ static bool vec_ok(const void* p, int64_t stride, int sz)
 template <int DT>
 static int launch_scan(const KParams& P, bool vec, bool longh, hipStream_t st)
 {
-    const dim3 grid(P.NT, P.a.rows);
+    const dim3 grid((P.NT + kWavesPerWG - 1) / kWavesPerWG, P.a.rows);
     if (vec) {
         if (longh) k_scan<DT, true, true><<<grid, kScanThreads, 0, st>>>(P);
         else k_scan<DT, true, false><<<grid, kScanThreads, 0, st>>>(P);
@@ -325,7 +327,7 @@ int fie_sampler_argmax(const void* logits, int32_t dtype, int32_t rows, int32_t 
     Ws w;
     int rc = ws_of(ws, rows, vocab, &w);
     if (rc != FIE_OK) return rc;
-    const int NT = (vocab + kTile - 1) / kTile;
+    const int NT = (vocab + kArgChunk - 1) / kArgChunk;
     const int sz = dtype == FIE_F32 ? 4 : 2;
     const bool vec = vec_ok(logits, row_stride, sz);
     hipStream_t st = (hipStream_t)stream;
@@ -354,7 +356,7 @@ int fie_sampler_kept(const fie_sampler_args* args, uint8_t* kept, float* probs,
     const int sz = args->dtype == FIE_F32 ? 4 : 2;
     const bool vec = vec_ok(args->logits, args->row_stride, sz);
     hipStream_t st = (hipStream_t)stream;
-    const dim3 grid(P.NT, args->rows);
+    const dim3 grid((args->vocab + kArgChunk - 1) / kArgChunk, args->rows);
 #define FIE_KEPT(DT)                                                                  \
     if (vec) k_kept<DT, true><<<grid, kScanThreads, 0, st>>>(P, kept, probs);        \
     else k_kept<DT, false><<<grid, kScanThreads, 0, st>>>(P, kept, probs);

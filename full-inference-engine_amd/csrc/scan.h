@@ -1,16 +1,20 @@
 // The streaming pass of the sampler (k_scan): one read of the logits.
 //
-// One workgroup of 256 threads per (tile, row); a tile is 8192 tokens held in
-// registers (32 per thread) after coalesced 128-bit loads.  Per tile it writes:
+// A tile is 2048 tokens, handled by one wave64 (32 tokens per lane, coalesced
+// 128-bit loads); a workgroup is four waves on four consecutive tiles of a row,
+// which share only the penalty-history count of their 8192-token span.  Per tile it
+// writes:
 //   maxc   (key << 32 | ~index) of the tile's largest penalised logit
 //   sw     sum of token weights floor(cexp(y - m_t) * 2^40) over the tile
 //          (rows that need the whole-row mass)
-//   cand   the tile's top tokens as (key, index) composites, every token whose key
-//          is >= bound; at least min(c, tile size) of them, at most kCap
+//   cand   the tile's top tokens as (key, index) composites: every token whose key
+//          is >= bound, at least min(c, tile size) of them, at most kCapW
 //   nu     distinct penalised ids inside the tile (the penalty scatter width)
 // Keys here are of the penalised logit x before temperature scaling: y = x / s is
 // non-decreasing in x, so the order, the maxima and the top tokens carry over and
-// the finish kernel converts the few values it needs.
+// the finish kernel converts the few values it needs.  Within a tile everything is
+// wave-local (DPP reductions, ballots); there is no barrier on rows without
+// penalties.
 #pragma once
 
 #include "common.h"
@@ -18,11 +22,15 @@
 
 namespace fie {
 
-constexpr int kScanThreads = 256;
-constexpr int kEPT = kTile / kScanThreads;   // tokens per thread
-constexpr int kCap = 128;                    // candidates per tile, at most
-constexpr int kCandMin = 64;                 // candidates per tile, at least (if present)
-constexpr int kMaxTiles = 64;                // vocab <= 64 * 8192
+constexpr int kScanThreads = 256;                // four waves, four tiles
+constexpr int kWavesPerWG = kScanThreads / 64;
+constexpr int kSpan = kTile * kWavesPerWG;       // tokens per workgroup (8192)
+constexpr int kEPT = kTile / 64;                 // tokens per lane (32)
+constexpr int kCapW = 64;                        // candidates per tile, at most
+constexpr int kCandMin = 16;                     // candidates per tile for rows without top-k
+constexpr int kStageW = 256;                     // tokens at or above a tile's floor, staged
+constexpr int kMaxTiles = 256;                   // vocab <= 256 * 2048
+constexpr int kHistPer = 8;                      // history ids per thread per batch
 
 // Result of one row kept for fie_sampler_kept().
 struct RowRes {
@@ -42,7 +50,7 @@ struct Ws {
     uint32_t* bound;     // [rows * NT]
     uint32_t* ncand;     // [rows * NT]
     uint32_t* nu;        // [rows * NT]
-    uint64_t* cand;      // [rows * NT * kCap]
+    uint64_t* cand;      // [rows * NT * kCapW]
     float* tok0x;        // [rows] token 0's logit (fp32, unpenalised)
     uint32_t* tok0c;     // [rows] occurrences of token 0 in the row's history
     uint32_t* bad;       // [rows] history ids >= vocab seen
@@ -120,83 +128,62 @@ FIE_DEV float y_of_xkey(uint32_t k, float s)
 }
 
 // Candidates per tile a row asks for: enough that the union over tiles holds the
-// row's top-k when the top tokens spread about evenly.
+// row's top-k when the top tokens spread about evenly, at least kCandMin.
 FIE_DEV uint32_t cand_target(int topk, int NT)
 {
     int c = kCandMin;
-    if (topk > 0) {
-        int need = 2 * ((topk + NT - 1) / NT) + 16;
-        c = need > c ? need : c;
-    }
-    return (uint32_t)(c < kCap ? c : kCap);
+    if (topk > 0) c = 2 * ((topk + NT - 1) / NT) + 4;
+    return (uint32_t)(c < 8 ? 8 : (c < kCapW ? c : kCapW));
 }
 
-// Descending selection over an LDS count histogram of NB bins (bin NB-1 = largest
-// keys): the bin holding the target-th largest element, the count above it and its
-// own count.  bin = -1 when fewer than `target` elements were counted.
-struct Pick {
-    int bin;
-    uint32_t above;
-    uint32_t inbin;
-};
+// Token index of lane element i of the wave's tile (group i / EPL is one 16-byte
+// load; groups are 64 * EPL tokens apart).
+template <int EPL>
+FIE_DEV int elem_index(int lo, int lane, int i) { return lo + ((i / EPL) * 64 + lane) * EPL + (i % EPL); }
 
-template <int NB, int NT>
-FIE_DEV Pick pick_desc(const uint32_t* h, uint32_t target, uint32_t* scratch, Pick* out)
+// Largest t (refining `pre` over bits hi..lo) with at least `target` of the keys
+// k[0..N) of the wave's lanes at or above t: a radix select by ballot counts.
+template <int N>
+FIE_DEV uint32_t ballot_select(const uint32_t (&k)[N], uint32_t target, uint32_t pre, int hi, int lo)
 {
-    constexpr int PER = NB / NT;
-    static_assert(PER >= 1 && NB % NT == 0, "bins per thread");
-    const int t = threadIdx.x;
-    uint32_t loc[PER];
-    uint32_t sum = 0;
+    for (int b = hi; b >= lo; --b) {
+        const uint32_t t = pre | (1u << b);
+        uint32_t cnt = 0;
 #pragma unroll
-    for (int q = 0; q < PER; ++q) {
-        loc[q] = h[NB - 1 - (t * PER + q)];
-        sum += loc[q];
+        for (int g = 0; g < N; ++g) cnt += popc64(__ballot(k[g] >= t));
+        if (cnt >= target) pre = t;
     }
-    uint32_t total;
-    uint32_t before = block_excl_scan_u32<NT>(sum, scratch, &total);
-    if (before < target && target <= before + sum) {
-        uint32_t run = before;
-#pragma unroll
-        for (int q = 0; q < PER; ++q) {
-            if (run < target && run + loc[q] >= target) {
-                out->bin = NB - 1 - (t * PER + q);
-                out->above = run;
-                out->inbin = loc[q];
-            }
-            run += loc[q];
-        }
-    }
-    if (t == 0 && total < target) {
-        out->bin = -1;
-        out->above = total;
-        out->inbin = 0;
-    }
-    __syncthreads();
-    Pick p = *out;
-    __syncthreads();
-    return p;
+    return pre;
 }
+
+// LDS of k_scan.
+template <bool LONGH>
+struct ScanSmem {
+    // penalty counts of the span's tokens: u16 halves (u32 words for long histories)
+    uint32_t cnt[LONGH ? kSpan : kSpan / 2];
+    uint32_t pbits[kSpan / 32];        // penalised tokens of the span, one bit each
+    uint64_t stage[kWavesPerWG][kStageW];
+    uint32_t zc, badc;
+    uint32_t uniq[kWavesPerWG];
+};
 
 // ---------------------------------------------------------------- k_scan
 template <int DT, bool VEC, bool LONGH>
 __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
 {
     constexpr int EPL = DTy<DT>::EPL, SZ = DTy<DT>::SZ, NL = kEPT / EPL;
-    // Penalty counts of the tile's tokens: u16 halves (u32 words for long histories).
-    constexpr int CW = LONGH ? kTile : kTile / 2;
-    __shared__ uint32_t cnt[CW];
-    __shared__ uint32_t hist[2048];
-    __shared__ uint32_t scr[32];
-    __shared__ Pick pick;
-    __shared__ uint32_t zc, badc, nc;
+    constexpr int CW = LONGH ? kSpan : kSpan / 2;
+    __shared__ ScanSmem<LONGH> L;
 
     const fie_sampler_args& a = P.a;
-    const int tile = blockIdx.x, row = blockIdx.y, tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int row = blockIdx.y;
     const int NT = P.NT, V = a.vocab;
+    const int slo = blockIdx.x * kSpan;                 // first token of the span
+    const int shi = min(slo + kSpan, V);
+    const int tile = blockIdx.x * kWavesPerWG + wv;     // this wave's tile
     const int lo = tile * kTile;
-    const int hi = min(lo + kTile, V);
-    const size_t slot = (size_t)row * NT + tile;
+    const bool live = tile < NT;                        // waves past the row's end idle
     const int32_t fl = a.flags[row];
     const bool greedy = fl & FIE_FLAG_GREEDY;
     const int lp = a.logprobs ? a.logprobs[row] : -1;
@@ -204,175 +191,245 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
     const int topk = greedy ? 0 : a.top_k[row];
     const bool need_mass = lp >= 0 || (!greedy && topk == 0);
     const bool need_cand = !greedy || lp > 0;
-    const float s = a.scale[row];
+    const float s = greedy ? 1.0f : a.scale[row];       // greedy rows stay unscaled (sampler.py:182)
     const char* rowp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * SZ;
+    const size_t slot = (size_t)row * NT + tile;
 
-    // 1. Issue every load of the tile before anything else.
+    // 1. The first history batch, then every load of the tile: the history is
+    //    counted while the logits are in flight.
+    uint32_t hid[kHistPer];
+    int64_t h0 = 0, h1 = 0;
+    if (pen) {
+        h0 = a.hist_offsets[row];
+        h1 = a.hist_offsets[row + 1];
+#pragma unroll
+        for (int q = 0; q < kHistPer; ++q) {
+            const int64_t h = h0 + q * kScanThreads + tid;
+            hid[q] = h < h1 ? (uint32_t)a.hist_ids[h] : 0xFFFFFFFFu;
+        }
+    }
     uint4 raw[NL];
 #pragma unroll
-    for (int j = 0; j < NL; ++j) raw[j] = load_group<DT, VEC>(rowp, lo + (j * kScanThreads + tid) * EPL, V);
+    for (int j = 0; j < NL; ++j)
+        raw[j] = live ? load_group<DT, VEC>(rowp, lo + (j * 64 + lane) * EPL, V) : make_uint4(0, 0, 0, 0);
 
-    // 2. Penalty counts of the tile's ids while the loads are in flight.
+    // 2. Penalty counts of the span's ids (sampler.py:134-144), shared by the four
+    //    waves.  A token's first count sets its bit in pbits and counts it as a
+    //    distinct id of its tile.
     float rep = 1.0f, pres = 0.0f, freq = 0.0f;
     if (pen) {
         rep = a.repetition[row];
         pres = a.presence[row];
         freq = a.frequency[row];
-        for (int i = tid; i < CW; i += kScanThreads) cnt[i] = 0;
-        if (tid == 0) { zc = 0; badc = 0; }
+        for (int i = tid; i < CW / 4; i += kScanThreads) ((uint4*)L.cnt)[i] = make_uint4(0, 0, 0, 0);
+        for (int i = tid; i < kSpan / 32; i += kScanThreads) L.pbits[i] = 0;
+        if (tid < kWavesPerWG) L.uniq[tid] = 0;
+        if (tid == 0) { L.zc = 0; L.badc = 0; }
         __syncthreads();
-        const int64_t h0 = a.hist_offsets[row], h1 = a.hist_offsets[row + 1];
-        for (int64_t h = h0 + tid; h < h1; h += kScanThreads) {
-            const uint32_t id = (uint32_t)a.hist_ids[h];
-            if (id >= (uint32_t)lo && id < (uint32_t)hi) {
-                const uint32_t o = id - lo;
-                if (id == 0) atomicAdd(&zc, 1u);
-                else if (LONGH) atomicAdd(&cnt[o], 1u);
-                else atomicAdd(&cnt[o >> 1], 1u << ((o & 1) * 16));
-            } else if (id >= (uint32_t)V && tile == NT - 1) {
-                atomicAdd(&badc, 1u);
+        for (int64_t base = h0; base < h1; base += (int64_t)kHistPer * kScanThreads) {
+            uint32_t ids[kHistPer];
+#pragma unroll
+            for (int q = 0; q < kHistPer; ++q) {
+                const int64_t h = base + q * kScanThreads + tid;
+                ids[q] = base == h0 ? hid[q] : (h < h1 ? (uint32_t)a.hist_ids[h] : 0xFFFFFFFFu);
+            }
+#pragma unroll
+            for (int q = 0; q < kHistPer; ++q) {
+                const uint32_t id = ids[q];
+                const int64_t h = base + q * kScanThreads + tid;
+                if (id >= (uint32_t)slo && id < (uint32_t)shi) {
+                    const uint32_t o = id - slo;
+                    if (id == 0) {
+                        atomicAdd(&L.zc, 1u);
+                    } else {
+                        uint32_t was;
+                        if (LONGH) {
+                            was = atomicAdd(&L.cnt[o], 1u);
+                        } else {
+                            const uint32_t sh = (o & 1) * 16;
+                            was = (atomicAdd(&L.cnt[o >> 1], 1u << sh) >> sh) & 0xFFFFu;
+                        }
+                        if (was == 0) {
+                            atomicOr(&L.pbits[o >> 5], 1u << (o & 31));
+                            atomicAdd(&L.uniq[o / kTile], 1u);
+                        }
+                    }
+                } else if (h < h1 && id >= (uint32_t)V && slo + kSpan >= V) {
+                    atomicAdd(&L.badc, 1u);
+                }
             }
         }
         __syncthreads();
-        uint32_t u = 0;
-        for (int i = tid; i < CW; i += kScanThreads) {
-            const uint32_t wv = cnt[i];
-            if (LONGH) u += wv != 0;
-            else u += ((wv & 0xFFFFu) != 0) + ((wv >> 16) != 0);
-        }
-        u = block_sum_u32<kScanThreads>(u, scr);
         if (tid == 0) {
-            P.w.nu[slot] = u;
-            if (tile == 0) P.w.tok0c[row] = zc;
-            if (tile == NT - 1) P.w.bad[row] = badc;
+            if (blockIdx.x == 0) P.w.tok0c[row] = L.zc;
+            if (slo + kSpan >= V) P.w.bad[row] = L.badc;
         }
-    } else if (tid == 0) {
-        P.w.nu[slot] = 0;
-        if (tile == 0) P.w.tok0c[row] = 0;
-        if (tile == NT - 1) P.w.bad[row] = 0;
+        if (live && lane == 0) P.w.nu[slot] = L.uniq[wv];
+    } else {
+        if (tid == 0) {
+            if (blockIdx.x == 0) P.w.tok0c[row] = 0;
+            if (slo + kSpan >= V) P.w.bad[row] = 0;
+        }
+        if (live && lane == 0) P.w.nu[slot] = 0;
     }
+    if (!live) return;
 
-    // 3. Penalised values and their order keys; token 0 and tokens past V get key 0
-    //    (token 0 is a tile of its own, settled by the finish kernel).
-    uint32_t key[kEPT];
+    // 3. The penalised logits (sampler.py:169-175) of the lane's tokens; the
+    //    group's bits of pbits say which tokens need their count looked up.
+    float x[kEPT];
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
-        const int e0 = lo + (j * kScanThreads + tid) * EPL;
-        uint32_t c[EPL];
-        if (pen) {
-            const int o = e0 - lo;
-            if (LONGH) {
 #pragma unroll
-                for (int e = 0; e < EPL; ++e) c[e] = (o + e < kTile) ? cnt[o + e] : 0u;
-            } else if constexpr (EPL == 8) {
-                const uint4 q = *(const uint4*)&cnt[o >> 1];
-                const uint32_t qq[4] = {q.x, q.y, q.z, q.w};
+        for (int e = 0; e < EPL; ++e) x[j * EPL + e] = lane_get<DT>(raw[j], e);
+    }
+    if (pen) {
+        uint32_t mine = 0;   // bit i: the lane's token i is penalised
 #pragma unroll
-                for (int e = 0; e < 8; ++e) c[e] = (qq[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-            } else {
-                const uint2 q = *(const uint2*)&cnt[o >> 1];
-                const uint32_t qq[2] = {q.x, q.y};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) c[e] = (qq[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu;
-            }
+        for (int j = 0; j < NL; ++j) {
+            const int o = lo - slo + (j * 64 + lane) * EPL;
+            mine |= ((L.pbits[o >> 5] >> (o & 31)) & ((1u << EPL) - 1)) << (j * EPL);
         }
-#pragma unroll
-        for (int e = 0; e < EPL; ++e) {
-            const int idx = e0 + e;
-            float x = lane_get<DT>(raw[j], e);
-            if (idx == 0) P.w.tok0x[row] = x;
-            if (pen && c[e]) x = penalize(x, rep, pres, freq, c[e]);
-            key[j * EPL + e] = (idx < V && idx != 0) ? fkey(x + 0.0f) : 0u;
+        for (uint32_t b = mine; b; b &= b - 1) {
+            const int i = __builtin_ctz(b);
+            const int o = lo - slo + ((i / EPL) * 64 + lane) * EPL + (i % EPL);
+            const uint32_t cc = LONGH ? L.cnt[o] : ((L.cnt[o >> 1] >> ((o & 1) * 16)) & 0xFFFFu);
+            x[i] = penalize(x[i], rep, pres, freq, cc);
         }
     }
-
-    // 4. Tile maximum and its first index.
-    uint32_t tm = 0;
-#pragma unroll
-    for (int i = 0; i < kEPT; ++i) tm = key[i] > tm ? key[i] : tm;
-    const uint32_t km = block_max_u32<kScanThreads>(tm, scr);
-    uint32_t fi = 0xFFFFFFFFu;
-#pragma unroll
-    for (int i = 0; i < kEPT; ++i) {
-        const uint32_t idx = (uint32_t)(lo + ((i / EPL) * kScanThreads + tid) * EPL + (i % EPL));
-        if (km != 0 && key[i] == km && idx < fi) fi = idx;
+    // Tokens outside the tile read NaN from here on: token 0 (a tile of its own,
+    // settled by the finish kernel) and tokens past the end of the row.  Every
+    // step below ignores NaN: fmax skips it, it equals nothing, cexp(NaN) is 0 and
+    // the staging test rejects it (NaN logits are outside the sampler's contract).
+    if (tile == 0 && lane == 0) {
+        P.w.tok0x[row] = lane_get<DT>(raw[0], 0);
+        x[0] = __builtin_nanf("");
     }
-    fi = block_min_u32<kScanThreads>(fi, scr);
-    if (tid == 0) P.w.maxc[slot] = km ? comp_key(km, fi) : 0ull;
-
-    // 5. Tile mass relative to the tile maximum (rule R1).
-    if (need_mass) {
-        uint64_t sum = 0;
-        if (km != 0) {
-            const float m = y_of_xkey(km, s);
-#pragma unroll
-            for (int i = 0; i < kEPT; ++i)
-                if (key[i]) sum += tok_weight(y_of_xkey(key[i], s), m);
-        }
-        sum = block_sum_u64<kScanThreads>(sum, (uint64_t*)scr);
-        if (tid == 0) P.w.sw[slot] = sum;
-    }
-
-    // 6. The tile's top tokens.  A floor first: the bin of the c-th largest
-    //    per-thread maximum, so at least c tokens lie above it and the histogram
-    //    sees only about c tokens instead of the whole tile.
-    if (need_cand) {
-        const uint32_t c = cand_target(topk, NT);
-        for (int i = tid; i < 2048; i += kScanThreads) hist[i] = 0;
-        if (tid == 0) nc = 0;
-        __syncthreads();
-        if (tm) atomicAdd(&hist[tm >> 21], 1u);
-        __syncthreads();
-        const Pick p0 = pick_desc<2048, kScanThreads>(hist, c, scr, &pick);
-        const uint32_t floor_key = p0.bin < 0 ? 1u : ((uint32_t)p0.bin << 21);
-        for (int i = tid; i < 2048; i += kScanThreads) hist[i] = 0;
-        __syncthreads();
+    if (lo + kTile > V) {
 #pragma unroll
         for (int i = 0; i < kEPT; ++i)
-            if (key[i] >= floor_key && key[i]) atomicAdd(&hist[key[i] >> 21], 1u);
-        __syncthreads();
-        const Pick p1 = pick_desc<2048, kScanThreads>(hist, c, scr, &pick);
-        uint32_t bound;
-        if (p1.bin < 0) {
-            bound = 1u;                                       // every token of the tile
-        } else if (p1.above + p1.inbin <= (uint32_t)kCap) {
-            bound = (uint32_t)p1.bin << 21;
-        } else {
-            for (int i = tid; i < 2048; i += kScanThreads) hist[i] = 0;
-            __syncthreads();
+            if (elem_index<EPL>(lo, lane, i) >= V) x[i] = __builtin_nanf("");
+    }
+
+    // 4. Group and lane maxima (float max: -0 and +0 compare equal, as their folded
+    //    keys do), the tile maximum's key, its first index.
+    constexpr int NG = NL;
+    float gm[NG];
 #pragma unroll
-            for (int i = 0; i < kEPT; ++i)
-                if ((key[i] >> 21) == (uint32_t)p1.bin) atomicAdd(&hist[(key[i] >> 10) & 0x7FFu], 1u);
-            __syncthreads();
-            const Pick p2 = pick_desc<2048, kScanThreads>(hist, c - p1.above, scr, &pick);
-            const uint32_t above2 = p1.above + p2.above;
-            const uint32_t pre2 = ((uint32_t)p1.bin << 11) | (uint32_t)p2.bin;
-            if (above2 + p2.inbin <= (uint32_t)kCap) {
-                bound = pre2 << 10;
+    for (int g = 0; g < NG; ++g) {
+        float v = x[g * EPL];
+#pragma unroll
+        for (int e = 1; e < EPL; ++e) v = __builtin_fmaxf(v, x[g * EPL + e]);
+        gm[g] = v;
+    }
+    float m = gm[0];
+#pragma unroll
+    for (int g = 1; g < NG; ++g) m = __builtin_fmaxf(m, gm[g]);
+    const uint32_t lkey = m == m ? fkey(m + 0.0f) : 0u;
+    const uint32_t km = dwave_max_u32(lkey);
+    uint32_t first = 0xFFFFFFFFu;
+    if (km != 0 && lkey == km) {
+        for (int i = kEPT - 1; i >= 0; --i)
+            if (x[i] == m) first = (uint32_t)elem_index<EPL>(lo, lane, i);
+    }
+    const uint32_t fi = dwave_min_u32(first);
+    if (lane == 0) P.w.maxc[slot] = km ? comp_key(km, fi) : 0ull;
+
+    // 5. Tile mass relative to the tile maximum (rule R1).  floor(e * 2^40) in two
+    //    32-bit halves of E = e * 2^8: hi = floor(E), lo = floor(frac(E) * 2^32),
+    //    both exact conversions of exact values.
+    if (need_mass) {
+        uint64_t slo64 = 0;
+        uint32_t shi32 = 0;
+        if (km != 0) {
+            const float mt = y_of_xkey(km, s);
+            auto acc = [&](float y) {
+                const float e = cexp_scaled(y - mt, 8);
+                const uint32_t h = (uint32_t)e;
+                const float f = (e - (float)h) * 4294967296.0f;
+                shi32 += h;
+                slo64 += (uint32_t)f;
+            };
+            if (s == 1.0f) {
+#pragma unroll
+                for (int i = 0; i < kEPT; ++i) acc(x[i] + 0.0f);
             } else {
-                for (int i = tid; i < 1024; i += kScanThreads) hist[i] = 0;
-                __syncthreads();
 #pragma unroll
-                for (int i = 0; i < kEPT; ++i)
-                    if ((key[i] >> 10) == pre2) atomicAdd(&hist[key[i] & 0x3FFu], 1u);
-                __syncthreads();
-                const Pick p3 = pick_desc<1024, kScanThreads>(hist, c - above2, scr, &pick);
-                const uint32_t K = (pre2 << 10) | (uint32_t)p3.bin;
-                bound = (above2 + p3.above + p3.inbin <= (uint32_t)kCap) ? K : K + 1u;
+                for (int i = 0; i < kEPT; ++i) acc(scaled(x[i], s));
             }
         }
-        uint64_t* out = P.w.cand + slot * kCap;
+        const uint64_t tot = dwave_sum_u64(((uint64_t)shi32 << 32) + slo64);
+        if (lane == 0) P.w.sw[slot] = tot;
+    }
+
+    // 6. The tile's top tokens.  The floor is the largest 12-bit key prefix with
+    //    at least c group maxima at or above it, so at least c tokens are; tokens
+    //    at or above it are staged in LDS, and when more than kCapW are, the c-th
+    //    largest staged key is found by a full-width ballot select.
+    if (need_cand) {
+        const uint32_t c = cand_target(topk, NT);
+        uint32_t gk[NG];
 #pragma unroll
-        for (int i = 0; i < kEPT; ++i) {
-            if (key[i] && key[i] >= bound) {
-                const uint32_t idx = (uint32_t)(lo + ((i / EPL) * kScanThreads + tid) * EPL + (i % EPL));
-                const uint32_t at = atomicAdd(&nc, 1u);
-                out[at] = comp_key(key[i], idx);
+        for (int g = 0; g < NG; ++g) gk[g] = gm[g] == gm[g] ? fkey(gm[g] + 0.0f) : 0u;
+        const uint32_t floor_key = ballot_select(gk, c, 0u, 31, 20);
+        // stage: per lane, its tokens at or above the floor
+        uint32_t mask = 0;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            if (gk[g] >= floor_key && gk[g] != 0) {
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const int i = g * EPL + e;
+                    if (x[i] == x[i] && fkey(x[i] + 0.0f) >= floor_key) mask |= 1u << i;
+                }
             }
         }
-        __syncthreads();
-        if (tid == 0) {
-            P.w.ncand[slot] = nc;
+        uint32_t E;
+        uint32_t at = dwave_excl_scan_u32((uint32_t)__builtin_popcount(mask), &E);
+        uint64_t* st = L.stage[wv];
+        for (uint32_t b = mask; b; b &= b - 1) {
+            const int i = __builtin_ctz(b);
+            if (at < (uint32_t)kStageW)
+                st[at] = comp_key(fkey(x[i] + 0.0f), (uint32_t)elem_index<EPL>(lo, lane, i));
+            ++at;
+        }
+        wave_lds_sync();
+        uint32_t bound = floor_key ? floor_key : 1u;
+        if (E > (uint32_t)kStageW) {
+            // more than kStageW tokens in the floor's bin (massive ties): emit
+            // nothing and mark the tile incomplete; the row takes the full-row path
+            bound = 0xFFFFFFFFu;
+            E = 0;
+        } else if (E > (uint32_t)kCapW) {
+            constexpr int SPL = kStageW / 64;
+            uint32_t sk[SPL];
+#pragma unroll
+            for (int q = 0; q < SPL; ++q) {
+                const uint32_t idx = (uint32_t)(q * 64 + lane);
+                sk[q] = idx < E ? comp_k(st[idx]) : 0u;
+            }
+            // the floor fixed the top 12 bits unless it stayed at 0 (fewer than c
+            // groups in the tile, all of them staged)
+            const uint32_t K = floor_key ? ballot_select(sk, c, floor_key & 0xFFF00000u, 19, 0)
+                                         : ballot_select(sk, c, 0u, 31, 0);
+            uint32_t ge = 0;
+#pragma unroll
+            for (int q = 0; q < SPL; ++q) ge += popc64(__ballot(sk[q] >= K));
+            bound = ge <= (uint32_t)kCapW ? K : K + 1u;       // ties beyond kCapW dropped
+        }
+        // emit the staged tokens with key >= bound (at most kCapW)
+        uint64_t* out = P.w.cand + slot * kCapW;
+        uint32_t nout = 0;
+        for (uint32_t q0 = 0; q0 < E; q0 += 64) {
+            const uint32_t idx = q0 + lane;
+            const uint64_t cc = idx < E ? st[idx] : 0ull;
+            const bool keep = idx < E && comp_k(cc) >= bound;
+            const uint64_t bal = __ballot(keep);
+            const uint32_t pos = nout + popc64(bal & ((1ull << lane) - 1));
+            if (keep && pos < (uint32_t)kCapW) out[pos] = cc;   // bound keeps pos < kCapW
+            nout += popc64(bal);
+        }
+        if (lane == 0) {
+            P.w.ncand[slot] = nout;
             P.w.bound[slot] = bound;
         }
     }

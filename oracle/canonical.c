@@ -43,7 +43,7 @@
 #include <stdlib.h>
 #include <string.h>
 
-#define FIE_TILE 8192
+#define FIE_TILE 2048
 typedef unsigned __int128 u128;
 
 /* ------------------------------------------------------------------ arithmetic */
