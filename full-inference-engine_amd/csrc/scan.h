@@ -328,36 +328,42 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
     const uint32_t km = dwave_max_u32(lkey);
     uint32_t first = 0xFFFFFFFFu;
     if (km != 0 && lkey == km) {
-        for (int i = kEPT - 1; i >= 0; --i)
-            if (x[i] == m) first = (uint32_t)elem_index<EPL>(lo, lane, i);
+        // groups lie in index order; the first group holding m, then its first token
+#pragma unroll
+        for (int g = 0; g < NG; ++g) {
+            if (first == 0xFFFFFFFFu && gm[g] == m) {
+#pragma unroll
+                for (int e = EPL - 1; e >= 0; --e)
+                    if (x[g * EPL + e] == m) first = (uint32_t)elem_index<EPL>(lo, lane, g * EPL + e);
+            }
+        }
     }
     const uint32_t fi = dwave_min_u32(first);
     if (lane == 0) P.w.maxc[slot] = km ? comp_key(km, fi) : 0ull;
 
-    // 5. Tile mass relative to the tile maximum (rule R1).  floor(e * 2^40) in two
-    //    32-bit halves of E = e * 2^8: hi = floor(E), lo = floor(frac(E) * 2^32),
-    //    both exact conversions of exact values.
+    // 5. Tile mass relative to the tile maximum (rule R1): the integer weights
+    //    floor(cexp(y - m_t) 2^40) < 2^41 as integer-valued floats, summed in fp64,
+    //    which is exact (a lane's 32 weights stay below 2^46).
     if (need_mass) {
-        uint64_t slo64 = 0;
-        uint32_t shi32 = 0;
+        double acc = 0.0;
         if (km != 0) {
             const float mt = y_of_xkey(km, s);
-            auto acc = [&](float y) {
-                const float e = cexp_scaled(y - mt, 8);
-                const uint32_t h = (uint32_t)e;
-                const float f = (e - (float)h) * 4294967296.0f;
-                shi32 += h;
-                slo64 += (uint32_t)f;
-            };
             if (s == 1.0f) {
 #pragma unroll
-                for (int i = 0; i < kEPT; ++i) acc(x[i] + 0.0f);
+                for (int i = 0; i < kEPT; ++i) acc += (double)weight40((x[i] + 0.0f) - mt);
+            } else if (s >= 0x1p-30f && s <= 0x1p30f) {
+                const float rs = 1.0f / s;
+#pragma unroll
+                for (int i = 0; i < kEPT; ++i) {
+                    const float y = markstein_ok(x[i]) ? div_markstein(x[i], s, rs) : x[i] / s;
+                    acc += (double)weight40((y + 0.0f) - mt);
+                }
             } else {
 #pragma unroll
-                for (int i = 0; i < kEPT; ++i) acc(scaled(x[i], s));
+                for (int i = 0; i < kEPT; ++i) acc += (double)weight40(scaled(x[i], s) - mt);
             }
         }
-        const uint64_t tot = dwave_sum_u64(((uint64_t)shi32 << 32) + slo64);
+        const uint64_t tot = dwave_sum_u64((uint64_t)acc);
         if (lane == 0) P.w.sw[slot] = tot;
     }
 
@@ -371,17 +377,16 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
 #pragma unroll
         for (int g = 0; g < NG; ++g) gk[g] = gm[g] == gm[g] ? fkey(gm[g] + 0.0f) : 0u;
         const uint32_t floor_key = ballot_select(gk, c, 0u, 31, 20);
-        // stage: per lane, its tokens at or above the floor
+        // stage: per lane, its tokens at or above the floor, by a float compare
+        // against the floor's value (NaN fails it); a floor whose value is not a
+        // number (a key of the NaN range) or 0 (all tokens) compares by key instead
+        const float fv = key_to_float(floor_key);
+        const bool fv_ok = floor_key > kKeyNegInf && floor_key <= kKeyPosInf;
         uint32_t mask = 0;
 #pragma unroll
-        for (int g = 0; g < NG; ++g) {
-            if (gk[g] >= floor_key && gk[g] != 0) {
-#pragma unroll
-                for (int e = 0; e < EPL; ++e) {
-                    const int i = g * EPL + e;
-                    if (x[i] == x[i] && fkey(x[i] + 0.0f) >= floor_key) mask |= 1u << i;
-                }
-            }
+        for (int i = 0; i < kEPT; ++i) {
+            const bool ge = fv_ok ? (x[i] >= fv) : (x[i] == x[i] && fkey(x[i] + 0.0f) >= floor_key);
+            mask |= ge ? (1u << i) : 0u;
         }
         uint32_t E;
         uint32_t at = dwave_excl_scan_u32((uint32_t)__builtin_popcount(mask), &E);
