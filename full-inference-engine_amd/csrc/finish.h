@@ -362,16 +362,31 @@ FIE_DEV SelResult row_select(FinSmem& S, const KParams& P, int row, float s, boo
     return SelResult{0, 0, 0, 0};
 }
 
-// Smallest y-key K with cexp(key_to_float(K) - M) >= mp (rule R5 as a threshold;
-// cexp is non-decreasing).  0 when mp <= 0.
+// Rule R5 as a threshold: L = the bound a 32-step bisection over the order keys of
+// d in [-80, 0] finds for cexp(d) >= mp, then the smallest y-key K with
+// fl(key_to_float(K) - M) >= L (monotone in K).  0 when mp <= 0.
+FIE_DEV float minp_bound(float mp)
+{
+    uint32_t lo = fkey(-80.0f), hi = fkey(0.0f);
+    if (cexp(key_to_float(lo)) >= mp) return -__builtin_inff();
+    while (hi - lo > 1) {
+        const uint32_t mid = lo + (hi - lo) / 2;
+        if (cexp(key_to_float(mid)) >= mp) hi = mid;
+        else lo = mid;
+    }
+    return key_to_float(hi);
+}
+
 FIE_DEV uint32_t minp_key(float M, float mp)
 {
     if (!(mp > 0.0f)) return 0;
+    const float L = minp_bound(mp);
     uint32_t lo = kKeyNegInf, hi = fkey(M);
-    if (!(cexp(key_to_float(hi) - M) >= mp)) return hi;   // degenerate rows (M not finite)
+    if ((key_to_float(lo) - M) >= L) return lo;          // every value passes
+    if (!((key_to_float(hi) - M) >= L)) return hi;       // degenerate rows (M not finite)
     while (hi - lo > 1) {
         const uint32_t mid = lo + (hi - lo) / 2;
-        if (cexp(key_to_float(mid) - M) >= mp) hi = mid;
+        if ((key_to_float(mid) - M) >= L) hi = mid;
         else lo = mid;
     }
     return hi;

@@ -26,7 +26,12 @@
  *                  evaluated exactly.
  *   (R4) draw      t = floor(u * K) with K the kept mass; the token is the first
  *                  kept token in (R2) order whose inclusive prefix mass exceeds t.
- *   (R5) min-p     a token is dropped iff cexp(y_i - M) < fp32(min_p).
+ *   (R5) min-p     a token is dropped iff fl(y_i - M) < L, where L is the fp32
+ *                  found by a 32-step bisection over order keys on [-80, 0] for
+ *                  the boundary of cexp(d) >= fp32(min_p) (oracle_minp_bound).
+ *                  Exactly the reference's probs < max(probs) * min_p in real
+ *                  arithmetic; the bisection makes the kept set a prefix of the
+ *                  value order even where cexp's last bit is not monotone.
  *   (R6) top_p==1  drops nothing (the exact-arithmetic reading of the reference's
  *                  `cumulative - p >= 1.0` test, sampler.py:226).
  *   (R7) logprobs  lse = M + ln(S_all) - 80 ln 2, S_all the mass of the whole row.
@@ -82,6 +87,36 @@ int64_t oracle_cexp_monotone_violations(float lo, float hi)
     return bad;
 }
 
+static inline float key_float(uint32_t k)
+{
+    uint32_t b = (k & 0x80000000u) ? (k & 0x7FFFFFFFu) : ~k;
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+static inline uint32_t fkey_(float y)
+{
+    uint32_t b;
+    memcpy(&b, &y, 4);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+/* Rule R5's bound: bisection over the order keys of d in [-80, 0] with the
+ * predicate cexp(d) >= mp (false at -80 unless mp is tiny, true at 0); returns the
+ * smallest d the bisection lands on, or -inf when every d passes. */
+float oracle_minp_bound(float mp)
+{
+    uint32_t lo = fkey_(-80.0f), hi = fkey_(0.0f);
+    if (oracle_cexp(key_float(lo)) >= mp) return -INFINITY;
+    while (hi - lo > 1) {
+        uint32_t mid = lo + (hi - lo) / 2;
+        if (oracle_cexp(key_float(mid)) >= mp) hi = mid;
+        else lo = mid;
+    }
+    return key_float(hi);
+}
+
 static inline uint64_t fixed40(float e)
 {
     return (uint64_t)((double)e * 1099511627776.0);   /* floor(e * 2^40), exact */
@@ -133,8 +168,7 @@ static u128 mul_shift(uint64_t m, u128 X, int q)
     return q ? ((v >> q) | ((u128)p2 << (128 - q))) : v;
 }
 
-/* Exact ceil(p * S) for an fp32 p in (0, 1) and S < 2^104 (so p's 24-bit
- * mantissa times S fits in 128 bits). */
+/* Exact ceil(p * S) for an fp32 p in (0, 1) and S < 2^128 (a 192-bit product). */
 static u128 ceil_mul_f32(float p, u128 S)
 {
     uint32_t b;
@@ -142,9 +176,16 @@ static u128 ceil_mul_f32(float p, u128 S)
     uint32_t eb = (b >> 23) & 0xFFu;
     uint64_t mant = (b & 0x7FFFFFu) | (eb ? 0x800000u : 0u);
     int q = eb ? 150 - (int)eb : 149;                    /* p = mant / 2^q, q >= 24 */
-    u128 P = (u128)mant * S;
-    if (q >= 128) return P ? 1 : 0;
-    return (P >> q) + (((P & ((((u128)1) << q) - 1)) != 0) ? 1 : 0);
+    u128 fl = mul_shift(mant, S, q);                     /* floor(mant S / 2^q) */
+    u128 low = mul_shift(mant, S, 0);                    /* mant S mod 2^128 */
+    int frac;
+    if (q < 128) {
+        frac = (low & ((((u128)1) << q) - 1)) != 0;
+    } else {
+        u128 mid = mul_shift(mant, S, 128);              /* mant S >> 128 */
+        frac = low != 0 || (mid & ((((u128)1) << (q - 128)) - 1)) != 0;
+    }
+    return fl + (frac ? 1 : 0);
 }
 
 /* Exact floor(u * K) for a double u in [0, 1) and K < 2^104. */
@@ -338,11 +379,12 @@ int32_t oracle_sample(oracle_args* a)
         }
         u128 sall = 0;
         for (int32_t i = 0; i < V; ++i) {
-            uint32_t kt = tmax[tile_of(i)];
+            const int t = tile_of(i);
+            uint32_t kt = tmax[t];
             uint32_t bits = (kt & 0x80000000u) ? (kt & 0x7FFFFFFFu) : ~kt;
             float mt;
             memcpy(&mt, &bits, 4);
-            w[i] = (u128)fixed40(oracle_cexp(y[i] - mt)) * tC[tile_of(i)];
+            w[i] = (u128)fixed40(oracle_cexp(y[i] - mt)) * tC[t];
             sall += w[i];
         }
         a->row_mass[2 * r] = (uint64_t)sall;
@@ -373,9 +415,10 @@ int32_t oracle_sample(oracle_args* a)
             }
             /* _filter min-p, sampler.py:211-218, rule (R5) */
             const float mp = a->min_p[r];
+            const float L = mp > 0.0f ? oracle_minp_bound(mp) : -INFINITY;
             u128 S = 0;
             for (int32_t i = 0; i < V; ++i) {
-                surv[i] = (fkey(y[i]) >= tk) && !(mp > 0.0f && oracle_cexp(y[i] - M) < mp);
+                surv[i] = (fkey(y[i]) >= tk) && !(mp > 0.0f && (y[i] - M) < L);
                 if (surv[i]) S += w[i];
             }
             /* _filter top-p, sampler.py:220-228, rules (R2)(R3)(R6) */
@@ -440,4 +483,57 @@ int32_t oracle_sample(oracle_args* a)
     }
     free(y); free(w); free(order); free(surv); free(tmax); free(tC);
     return 0;
+}
+
+/* ------------------------------------------------------------------ division check */
+
+static float f16_to_f32(uint16_t h)
+{
+    uint32_t sgn = (h >> 15) & 1u, e = (h >> 10) & 31u, m = h & 1023u;
+    float v;
+    if (e == 0) v = ldexpf((float)m, -24);
+    else if (e == 31) v = m ? NAN : INFINITY;
+    else v = ldexpf((float)(m | 1024u), (int)e - 25);
+    return sgn ? -v : v;
+}
+
+static float markstein(float x, float s, float r)
+{
+    float q = x * r;
+    float e = fmaf(-q, s, x);
+    return fmaf(e, r, q);
+}
+
+/* The HIP kernels divide by the temperature with Markstein's correction
+ * q = RN(x r), e = x - q s, RN(q + e r) from r = RN(1/s) when 2^-96 <= |x| <= 2^96
+ * and 2^-30 <= s <= 2^30.  Counts, for one s, the inputs in that range where it
+ * differs from the IEEE quotient: every fp16 value, every bf16 value, and
+ * `nrandom` pseudo-random fp32 values (xorshift from `seed`). */
+int64_t oracle_markstein_mismatches(float s, int64_t nrandom, uint32_t seed)
+{
+    const float r = 1.0f / s;
+    int64_t bad = 0;
+    for (uint32_t h = 0; h < 65536u; ++h) {
+        float xs[2];
+        uint32_t bb = h << 16;
+        xs[0] = f16_to_f32((uint16_t)h);
+        memcpy(&xs[1], &bb, 4);
+        for (int k = 0; k < 2; ++k) {
+            float x = xs[k], a = fabsf(x);
+            if (!(a >= 0x1p-96f && a <= 0x1p96f)) continue;
+            float q1 = x / s, q2 = markstein(x, s, r);
+            if (memcmp(&q1, &q2, 4) != 0) ++bad;
+        }
+    }
+    uint32_t st = seed ? seed : 1u;
+    for (int64_t i = 0; i < nrandom; ++i) {
+        st ^= st << 13; st ^= st >> 17; st ^= st << 5;
+        uint32_t e = 31u + (st % 193u);                  /* exponents 2^-96 .. 2^96 */
+        uint32_t bits = (st & 0x807FFFFFu) | (e << 23);
+        float x;
+        memcpy(&x, &bits, 4);
+        float q1 = x / s, q2 = markstein(x, s, r);
+        if (memcmp(&q1, &q2, 4) != 0) ++bad;
+    }
+    return bad;
 }

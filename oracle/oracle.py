@@ -51,12 +51,27 @@ def _load():
         _lib.oracle_penalize.restype = ctypes.c_int32
         _lib.oracle_cexp_monotone_violations.restype = ctypes.c_int64
         _lib.oracle_cexp_monotone_violations.argtypes = [ctypes.c_float, ctypes.c_float]
+        _lib.oracle_minp_bound.restype = ctypes.c_float
+        _lib.oracle_minp_bound.argtypes = [ctypes.c_float]
+        _lib.oracle_markstein_mismatches.restype = ctypes.c_int64
+        _lib.oracle_markstein_mismatches.argtypes = [ctypes.c_float, ctypes.c_int64, ctypes.c_uint32]
     return _lib
 
 
 def cexp_monotone_violations(lo: float, hi: float) -> int:
     """Adjacent fp32 pairs in [lo, hi] where the canonical exponential decreases."""
     return int(_load().oracle_cexp_monotone_violations(lo, hi))
+
+
+def minp_bound(mp: float) -> float:
+    """Rule R5's bound L: a token survives min-p iff fl(y - M) >= L."""
+    return float(_load().oracle_minp_bound(mp))
+
+
+def markstein_mismatches(s: float, nrandom: int = 1_000_000, seed: int = 1) -> int:
+    """Inputs in the guarded range where the kernels' Markstein-corrected divide by
+    `s` differs from the IEEE quotient (all fp16, all bf16, `nrandom` fp32)."""
+    return int(_load().oracle_markstein_mismatches(s, nrandom, seed))
 
 
 def cexp(values: np.ndarray) -> np.ndarray:
