@@ -146,7 +146,7 @@ static int fail(int code, const char* msg)
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Layout {
-    size_t maxc, sw, bound, ncand, nu, cand, tok0x, tok0c, bad, res, mt, ct, total;
+    size_t maxc, sw, bound, ncand, nu, nb, bk, cand, tok0x, tok0c, bad, res, mt, ct, total;
 };
 
 static bool layout_of(int32_t R, int32_t V, Layout* L)
@@ -161,6 +161,9 @@ static bool layout_of(int32_t R, int32_t V, Layout* L)
     L->bound = take(r * NT * 4);
     L->ncand = take(r * NT * 4);
     L->nu = take(r * NT * 4);
+    const size_t NS = (NT + kWavesPerWG - 1) / kWavesPerWG;
+    L->nb = take(r * NS * 4);
+    L->bk = take(r * NS * kBucketCap * 2);
     L->cand = take(r * NT * kCapW * 8);
     L->tok0x = take(r * 4);
     L->tok0c = take(r * 4);
@@ -189,6 +192,8 @@ static int ws_of(const fie_workspace* ws, int32_t rows, int32_t V, Ws* w)
     w->bound = (uint32_t*)(b + L.bound);
     w->ncand = (uint32_t*)(b + L.ncand);
     w->nu = (uint32_t*)(b + L.nu);
+    w->nb = (uint32_t*)(b + L.nb);
+    w->bk = (uint16_t*)(b + L.bk);
     w->cand = (uint64_t*)(b + L.cand);
     w->tok0x = (float*)(b + L.tok0x);
     w->tok0c = (uint32_t*)(b + L.tok0c);
@@ -234,7 +239,11 @@ static bool vec_ok(const void* p, int64_t stride, int sz)
 template <int DT>
 static int launch_scan(const KParams& P, bool vec, bool longh, hipStream_t st)
 {
-    const dim3 grid((P.NT + kWavesPerWG - 1) / kWavesPerWG, P.a.rows);
+    if (P.a.apply_penalties) {
+        k_prep<<<P.a.rows, kPrepThreads, 0, st>>>(P);
+        FIE_LAUNCH_CHECK("k_prep");
+    }
+    const dim3 grid(P.NS, P.a.rows);
     if (vec) {
         if (longh) k_scan<DT, true, true><<<grid, kScanThreads, 0, st>>>(P);
         else k_scan<DT, true, false><<<grid, kScanThreads, 0, st>>>(P);
@@ -280,6 +289,7 @@ static int prepare(const fie_sampler_args* args, const fie_workspace* ws, KParam
     if (rc != FIE_OK) return rc;
     P->a = *args;
     P->NT = (args->vocab + kTile - 1) / kTile;
+    P->NS = (P->NT + kWavesPerWG - 1) / kWavesPerWG;
     if (args->rows == 0) return FIE_OK;
     return ws_of(ws, args->rows, args->vocab, &P->w);
 }

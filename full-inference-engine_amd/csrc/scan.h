@@ -30,7 +30,10 @@ constexpr int kCapW = 64;                        // candidates per tile, at most
 constexpr int kCandMin = 16;                     // candidates per tile for rows without top-k
 constexpr int kStageW = 256;                     // tokens at or above a tile's floor, staged
 constexpr int kMaxTiles = 256;                   // vocab <= 256 * 2048
-constexpr int kHistPer = 8;                      // history ids per thread per batch
+constexpr int kBucketCap = 512;                  // history ids of one span held by k_prep
+constexpr int kMaxSpans = kMaxTiles / kWavesPerWG;
+constexpr int kPrepThreads = 256;
+constexpr int kPS = 4;                           // penalised tokens per lane held in slots
 
 // Result of one row kept for fie_sampler_kept().
 struct RowRes {
@@ -50,6 +53,8 @@ struct Ws {
     uint32_t* bound;     // [rows * NT]
     uint32_t* ncand;     // [rows * NT]
     uint32_t* nu;        // [rows * NT]
+    uint32_t* nb;        // [rows * NS] history ids (other than 0) falling in each span
+    uint16_t* bk;        // [rows * NS * kBucketCap] their offsets in the span (first kBucketCap)
     uint64_t* cand;      // [rows * NT * kCapW]
     float* tok0x;        // [rows] token 0's logit (fp32, unpenalised)
     uint32_t* tok0c;     // [rows] occurrences of token 0 in the row's history
@@ -63,6 +68,7 @@ struct KParams {
     fie_sampler_args a;
     Ws w;
     int NT;
+    int NS;              // spans of kSpan tokens per row
 };
 
 // ---------------------------------------------------------------- element access
@@ -108,6 +114,18 @@ FIE_DEV uint4 load_group(const char* rowp, int e0, int V)
         }
     }
     return r;
+}
+
+// Token idx of a row, as fp32.
+template <int DT>
+FIE_DEV float load_elem(const char* rowp, uint32_t idx)
+{
+    if constexpr (DT == FIE_F32) {
+        return ((const float*)rowp)[idx];
+    } else {
+        const uint32_t h = ((const uint16_t*)rowp)[idx];
+        return lane_get<DT>(make_uint4(h, 0, 0, 0), 0);
+    }
 }
 
 // sampler.py:169-173, one element: transformers' repetition convention, then the
@@ -163,9 +181,47 @@ struct ScanSmem {
     uint32_t cnt[LONGH ? kSpan : kSpan / 2];
     uint32_t pbits[kSpan / 32];        // penalised tokens of the span, one bit each
     uint64_t stage[kWavesPerWG][kStageW];
-    uint32_t zc, badc;
     uint32_t uniq[kWavesPerWG];
 };
+
+// ---------------------------------------------------------------- k_prep
+// Buckets the history of every penalised row by span (sampler.py:134-144 counts
+// the same ids): the offsets inside the span of the first kBucketCap ids of each
+// span, the number of ids per span, the occurrences of token 0 and of ids >= vocab.
+// Each k_scan workgroup then reads its own span's bucket instead of the whole
+// history.  The order inside a bucket is free: only counts are taken from it.
+__global__ __launch_bounds__(kPrepThreads) void k_prep(const KParams P)
+{
+    __shared__ uint32_t sc[kMaxSpans];
+    __shared__ uint32_t zc, badc;
+    const fie_sampler_args& a = P.a;
+    const int row = blockIdx.x, tid = threadIdx.x, NS = P.NS;
+    const uint32_t V = (uint32_t)a.vocab;
+    if (!(a.apply_penalties && (a.flags[row] & FIE_FLAG_PENALTY))) return;
+    if (tid < NS) sc[tid] = 0;
+    if (tid == 0) { zc = 0; badc = 0; }
+    __syncthreads();
+    const int64_t h0 = a.hist_offsets[row], h1 = a.hist_offsets[row + 1];
+    uint16_t* bk = P.w.bk + (size_t)row * NS * kBucketCap;
+    for (int64_t h = h0 + tid; h < h1; h += kPrepThreads) {
+        const uint32_t id = (uint32_t)a.hist_ids[h];
+        if (id == 0) {
+            atomicAdd(&zc, 1u);
+        } else if (id < V) {
+            const uint32_t sp = id / (uint32_t)kSpan;
+            const uint32_t at = atomicAdd(&sc[sp], 1u);
+            if (at < (uint32_t)kBucketCap) bk[sp * kBucketCap + at] = (uint16_t)(id % (uint32_t)kSpan);
+        } else {
+            atomicAdd(&badc, 1u);
+        }
+    }
+    __syncthreads();
+    if (tid < NS) P.w.nb[(size_t)row * NS + tid] = sc[tid];
+    if (tid == 0) {
+        P.w.tok0c[row] = zc;
+        P.w.bad[row] = badc;
+    }
+}
 
 // ---------------------------------------------------------------- k_scan
 template <int DT, bool VEC, bool LONGH>
@@ -195,18 +251,13 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
     const char* rowp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * SZ;
     const size_t slot = (size_t)row * NT + tile;
 
-    // 1. The first history batch, then every load of the tile: the history is
-    //    counted while the logits are in flight.
-    uint32_t hid[kHistPer];
-    int64_t h0 = 0, h1 = 0;
+    // 1. The span's history bucket (k_prep), then every load of the tile: the
+    //    history is counted while the logits are in flight.
+    const size_t rs = (size_t)row * P.NS + blockIdx.x;
+    uint32_t nb = 0, e0 = 0;
     if (pen) {
-        h0 = a.hist_offsets[row];
-        h1 = a.hist_offsets[row + 1];
-#pragma unroll
-        for (int q = 0; q < kHistPer; ++q) {
-            const int64_t h = h0 + q * kScanThreads + tid;
-            hid[q] = h < h1 ? (uint32_t)a.hist_ids[h] : 0xFFFFFFFFu;
-        }
+        nb = P.w.nb[rs];
+        e0 = P.w.bk[rs * kBucketCap + tid];
     }
     uint4 raw[NL];
 #pragma unroll
@@ -215,7 +266,8 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
 
     // 2. Penalty counts of the span's ids (sampler.py:134-144), shared by the four
     //    waves.  A token's first count sets its bit in pbits and counts it as a
-    //    distinct id of its tile.
+    //    distinct id of its tile.  A bucket that overflowed (more than kBucketCap
+    //    ids in the span) is replaced by a scan of the row's whole history.
     float rep = 1.0f, pres = 0.0f, freq = 0.0f;
     if (pen) {
         rep = a.repetition[row];
@@ -224,64 +276,54 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
         for (int i = tid; i < CW / 4; i += kScanThreads) ((uint4*)L.cnt)[i] = make_uint4(0, 0, 0, 0);
         for (int i = tid; i < kSpan / 32; i += kScanThreads) L.pbits[i] = 0;
         if (tid < kWavesPerWG) L.uniq[tid] = 0;
-        if (tid == 0) { L.zc = 0; L.badc = 0; }
         __syncthreads();
-        for (int64_t base = h0; base < h1; base += (int64_t)kHistPer * kScanThreads) {
-            uint32_t ids[kHistPer];
-#pragma unroll
-            for (int q = 0; q < kHistPer; ++q) {
-                const int64_t h = base + q * kScanThreads + tid;
-                ids[q] = base == h0 ? hid[q] : (h < h1 ? (uint32_t)a.hist_ids[h] : 0xFFFFFFFFu);
+        auto count = [&](uint32_t o) {
+            uint32_t was;
+            if (LONGH) {
+                was = atomicAdd(&L.cnt[o], 1u);
+            } else {
+                const uint32_t sh = (o & 1) * 16;
+                was = (atomicAdd(&L.cnt[o >> 1], 1u << sh) >> sh) & 0xFFFFu;
             }
-#pragma unroll
-            for (int q = 0; q < kHistPer; ++q) {
-                const uint32_t id = ids[q];
-                const int64_t h = base + q * kScanThreads + tid;
-                if (id >= (uint32_t)slo && id < (uint32_t)shi) {
-                    const uint32_t o = id - slo;
-                    if (id == 0) {
-                        atomicAdd(&L.zc, 1u);
-                    } else {
-                        uint32_t was;
-                        if (LONGH) {
-                            was = atomicAdd(&L.cnt[o], 1u);
-                        } else {
-                            const uint32_t sh = (o & 1) * 16;
-                            was = (atomicAdd(&L.cnt[o >> 1], 1u << sh) >> sh) & 0xFFFFu;
-                        }
-                        if (was == 0) {
-                            atomicOr(&L.pbits[o >> 5], 1u << (o & 31));
-                            atomicAdd(&L.uniq[o / kTile], 1u);
-                        }
-                    }
-                } else if (h < h1 && id >= (uint32_t)V && slo + kSpan >= V) {
-                    atomicAdd(&L.badc, 1u);
-                }
+            if (was == 0) {
+                atomicOr(&L.pbits[o >> 5], 1u << (o & 31));
+                atomicAdd(&L.uniq[o / kTile], 1u);
+            }
+        };
+        if (nb <= (uint32_t)kBucketCap) {
+            if ((uint32_t)tid < nb) count(e0);
+            for (uint32_t i = tid + kScanThreads; i < nb; i += kScanThreads) count(P.w.bk[rs * kBucketCap + i]);
+        } else {
+            const int64_t h0 = a.hist_offsets[row], h1 = a.hist_offsets[row + 1];
+            for (int64_t h = h0 + tid; h < h1; h += kScanThreads) {
+                const uint32_t id = (uint32_t)a.hist_ids[h];
+                if (id != 0 && id >= (uint32_t)slo && id < (uint32_t)shi) count(id - (uint32_t)slo);
             }
         }
         __syncthreads();
-        if (tid == 0) {
-            if (blockIdx.x == 0) P.w.tok0c[row] = L.zc;
-            if (slo + kSpan >= V) P.w.bad[row] = L.badc;
-        }
         if (live && lane == 0) P.w.nu[slot] = L.uniq[wv];
     } else {
-        if (tid == 0) {
-            if (blockIdx.x == 0) P.w.tok0c[row] = 0;
-            if (slo + kSpan >= V) P.w.bad[row] = 0;
-        }
         if (live && lane == 0) P.w.nu[slot] = 0;
     }
     if (!live) return;
 
-    // 3. The penalised logits (sampler.py:169-175) of the lane's tokens; the
-    //    group's bits of pbits say which tokens need their count looked up.
+    // 3. The penalised logits (sampler.py:169-175).  Registers are indexed only
+    //    statically (a runtime index into x[] turns into a select per element):
+    //    the lane's penalised tokens read NaN in x[] and are re-read from memory
+    //    (the lines were just fetched) into up to kPS slots, penalised there, and
+    //    join the maximum, the mass and the staging as extra elements.  A wave
+    //    with a lane holding more than kPS penalised tokens patches x[] in place.
     float x[kEPT];
 #pragma unroll
     for (int j = 0; j < NL; ++j) {
 #pragma unroll
         for (int e = 0; e < EPL; ++e) x[j * EPL + e] = lane_get<DT>(raw[j], e);
     }
+    float pv[kPS];           // penalised values of the slots (NaN = empty)
+    uint32_t pidx[kPS];      // their token indices
+#pragma unroll
+    for (int q = 0; q < kPS; ++q) { pv[q] = __builtin_nanf(""); pidx[q] = 0xFFFFFFFFu; }
+    bool odd = false;        // a patched value outside the unchecked divide's range
     if (pen) {
         uint32_t mine = 0;   // bit i: the lane's token i is penalised
 #pragma unroll
@@ -289,11 +331,36 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
             const int o = lo - slo + (j * 64 + lane) * EPL;
             mine |= ((L.pbits[o >> 5] >> (o & 31)) & ((1u << EPL) - 1)) << (j * EPL);
         }
-        for (uint32_t b = mine; b; b &= b - 1) {
-            const int i = __builtin_ctz(b);
-            const int o = lo - slo + ((i / EPL) * 64 + lane) * EPL + (i % EPL);
-            const uint32_t cc = LONGH ? L.cnt[o] : ((L.cnt[o >> 1] >> ((o & 1) * 16)) & 0xFFFFu);
-            x[i] = penalize(x[i], rep, pres, freq, cc);
+        auto count_of = [&](int o) -> uint32_t {
+            return LONGH ? L.cnt[o] : ((L.cnt[o >> 1] >> ((o & 1) * 16)) & 0xFFFFu);
+        };
+        if (__ballot(__builtin_popcount(mine) > kPS) != 0) {
+            for (uint32_t b = mine; b; b &= b - 1) {
+                const int i = __builtin_ctz(b);
+                const int o = lo - slo + ((i / EPL) * 64 + lane) * EPL + (i % EPL);
+                x[i] = penalize(x[i], rep, pres, freq, count_of(o));
+                // a finite, nonzero value outside Markstein's range (extreme penalty
+                // parameters) sends the wave's fp16 mass loop to the checked divide
+                if (!(markstein_ok(x[i]) || x[i] == 0.0f || !__builtin_isfinite(x[i]))) odd = true;
+            }
+        } else if (__ballot(mine != 0) != 0) {
+#pragma unroll
+            for (int i = 0; i < kEPT; ++i)
+                if ((mine >> i) & 1u) x[i] = __builtin_nanf("");
+            uint32_t b = mine;
+#pragma unroll
+            for (int q = 0; q < kPS; ++q) {
+                if (b) {
+                    pidx[q] = (uint32_t)elem_index<EPL>(lo, lane, __builtin_ctz(b));
+                    b &= b - 1;
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < kPS; ++q)
+                if (pidx[q] != 0xFFFFFFFFu) pv[q] = load_elem<DT>(rowp, pidx[q]);
+#pragma unroll
+            for (int q = 0; q < kPS; ++q)
+                if (pidx[q] != 0xFFFFFFFFu) pv[q] = penalize(pv[q], rep, pres, freq, count_of((int)pidx[q] - slo));
         }
     }
     // Tokens outside the tile read NaN from here on: token 0 (a tile of its own,
@@ -324,6 +391,8 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
     float m = gm[0];
 #pragma unroll
     for (int g = 1; g < NG; ++g) m = __builtin_fmaxf(m, gm[g]);
+#pragma unroll
+    for (int q = 0; q < kPS; ++q) m = __builtin_fmaxf(m, pv[q]);
     const uint32_t lkey = m == m ? fkey(m + 0.0f) : 0u;
     const uint32_t km = dwave_max_u32(lkey);
     uint32_t first = 0xFFFFFFFFu;
@@ -337,31 +406,52 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
                     if (x[g * EPL + e] == m) first = (uint32_t)elem_index<EPL>(lo, lane, g * EPL + e);
             }
         }
+#pragma unroll
+        for (int q = 0; q < kPS; ++q)
+            if (pv[q] == m && pidx[q] < first) first = pidx[q];
     }
     const uint32_t fi = dwave_min_u32(first);
     if (lane == 0) P.w.maxc[slot] = km ? comp_key(km, fi) : 0ull;
 
     // 5. Tile mass relative to the tile maximum (rule R1): the integer weights
     //    floor(cexp(y - m_t) 2^40) < 2^41 as integer-valued floats, summed in fp64,
-    //    which is exact (a lane's 32 weights stay below 2^46).
+    //    which is exact (a lane's 32 weights stay below 2^46).  y - m_t needs no
+    //    folding of -0: both zeros give the same difference.  The temperature
+    //    divide is Markstein's corrected product, equal to the IEEE quotient while
+    //    2^-96 <= |x| <= 2^96 and 2^-30 <= s <= 2^30: always so for finite,
+    //    nonzero fp16 logits; 0 gives 0; +-inf and NaN give NaN there and weight 0
+    //    through cexp's clamp, as the IEEE quotient's weight does.  Only penalised
+    //    values can leave the range, and the patch step flags them.
     if (need_mass) {
         double acc = 0.0;
         if (km != 0) {
             const float mt = y_of_xkey(km, s);
             if (s == 1.0f) {
 #pragma unroll
-                for (int i = 0; i < kEPT; ++i) acc += (double)weight40((x[i] + 0.0f) - mt);
+                for (int i = 0; i < kEPT; ++i) acc += (double)weight40(x[i] - mt);
             } else if (s >= 0x1p-30f && s <= 0x1p30f) {
                 const float rs = 1.0f / s;
+                if (DT == FIE_F16 && __ballot(odd) == 0) {
 #pragma unroll
-                for (int i = 0; i < kEPT; ++i) {
-                    const float y = markstein_ok(x[i]) ? div_markstein(x[i], s, rs) : x[i] / s;
-                    acc += (double)weight40((y + 0.0f) - mt);
+                    for (int i = 0; i < kEPT; ++i) acc += (double)weight40(div_markstein(x[i], s, rs) - mt);
+                } else {
+#pragma unroll
+                    for (int i = 0; i < kEPT; ++i) {
+                        const float y = markstein_ok(x[i]) ? div_markstein(x[i], s, rs) : x[i] / s;
+                        acc += (double)weight40(y - mt);
+                    }
                 }
             } else {
 #pragma unroll
                 for (int i = 0; i < kEPT; ++i) acc += (double)weight40(scaled(x[i], s) - mt);
             }
+        }
+        if (km != 0) {
+            const float mt = y_of_xkey(km, s);
+#pragma unroll
+            for (int q = 0; q < kPS; ++q)
+                if (__ballot(pidx[q] != 0xFFFFFFFFu) != 0)
+                    acc += (double)weight40((s == 1.0f ? pv[q] : scaled(pv[q], s)) - mt);
         }
         const uint64_t tot = dwave_sum_u64((uint64_t)acc);
         if (lane == 0) P.w.sw[slot] = tot;
@@ -388,14 +478,29 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
             const bool ge = fv_ok ? (x[i] >= fv) : (x[i] == x[i] && fkey(x[i] + 0.0f) >= floor_key);
             mask |= ge ? (1u << i) : 0u;
         }
+        uint32_t pmask = 0;      // slots at or above the floor
+#pragma unroll
+        for (int q = 0; q < kPS; ++q) {
+            const bool ge = fv_ok ? (pv[q] >= fv) : (pv[q] == pv[q] && fkey(pv[q] + 0.0f) >= floor_key);
+            pmask |= ge ? (1u << q) : 0u;
+        }
         uint32_t E;
-        uint32_t at = dwave_excl_scan_u32((uint32_t)__builtin_popcount(mask), &E);
+        uint32_t at = dwave_excl_scan_u32((uint32_t)(__builtin_popcount(mask) + __builtin_popcount(pmask)), &E);
         uint64_t* st = L.stage[wv];
         for (uint32_t b = mask; b; b &= b - 1) {
             const int i = __builtin_ctz(b);
             if (at < (uint32_t)kStageW)
                 st[at] = comp_key(fkey(x[i] + 0.0f), (uint32_t)elem_index<EPL>(lo, lane, i));
             ++at;
+        }
+        if (__ballot(pmask != 0) != 0) {
+#pragma unroll
+            for (int q = 0; q < kPS; ++q) {
+                if ((pmask >> q) & 1u) {
+                    if (at < (uint32_t)kStageW) st[at] = comp_key(fkey(pv[q] + 0.0f), pidx[q]);
+                    ++at;
+                }
+            }
         }
         wave_lds_sync();
         uint32_t bound = floor_key ? floor_key : 1u;
