@@ -13,6 +13,13 @@
 
 namespace fie {
 
+#ifdef FIE_PHASE_PROFILE
+__device__ uint64_t g_fie_prof[8192 * 16];
+#define FIE_MARK(i) do { if (threadIdx.x == 0 && blockIdx.x < 8192) g_fie_prof[(size_t)blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memtime(); } while (0)
+#else
+#define FIE_MARK(i) do { } while (0)
+#endif
+
 constexpr int kFinThreads = 512;
 constexpr int kGCap = 8192 + 64;   // composites held in LDS (candidates / a gathered bin)
 constexpr int kPassBins = 2048;    // bins of a full-row radix pass
@@ -51,6 +58,7 @@ struct FinSmem {
     uint64_t bcomp[2];
     u128 bex, bme;
     uint32_t bcnt;
+    uint64_t cmax;
     SelResult sel;
 };
 
@@ -392,6 +400,196 @@ FIE_DEV uint32_t minp_key(float M, float mp)
     return hi;
 }
 
+// ---------------------------------------------------------------- binned full-row path
+// Bins of a row by d = fl(M - y) at kDQ bins per unit (the last bin takes d >= 32
+// and NaN).  fl(M - y) and the scaling by a power of two are monotone, so bins lie
+// in rule R2 order: a lower bin holds only larger values, and ties share a bin.
+constexpr float kDQ = 64.0f;
+
+FIE_DEV int dbin_key(float M, uint32_t key)
+{
+    const float q = (M - key_to_float(key)) * kDQ;
+    return q < (float)(kPassBins - 1) ? (int)q : kPassBins - 1;
+}
+
+FIE_DEV u128 bin_mass(const FinSmem& S, int b) { return ((u128)S.pm_hi[b] << 64) | S.pm_lo[b]; }
+
+// Ascending scan of bins [0, bmax], bin bmax measuring `last` instead of its own
+// total, for the bin where the running measure (count, or mass when MASS) first
+// exceeds g; -1 when the total is <= g.  *above receives the measure before it
+// (the total when -1).
+template <bool MASS>
+FIE_DEV int dbin_pick(FinSmem& S, int bmax, u128 last, u128 g, u128* above)
+{
+    constexpr int per = kPassBins / kFinThreads;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    auto meas = [&](int b) -> u128 {
+        if (b > bmax) return 0;
+        if (b == bmax) return last;
+        return MASS ? bin_mass(S, b) : (u128)S.pc[b];
+    };
+    u128 sum = 0;
+#pragma unroll
+    for (int q = 0; q < per; ++q) sum += meas(tid * per + q);
+    const u128 incl = wave_incl_scan_u128(sum);
+    if (lane == 63) S.red128[wave] = incl;
+    if (tid == 0) S.ibin = -1;
+    __syncthreads();
+    u128 before = 0, all = 0;
+    for (int w = 0; w < kFinThreads / 64; ++w) {
+        if (w < wave) before += S.red128[w];
+        all += S.red128[w];
+    }
+    before += incl - sum;
+    if (before <= g && g < before + sum) {
+        u128 run = before;
+#pragma unroll
+        for (int q = 0; q < per; ++q) {
+            const u128 m = meas(tid * per + q);
+            if (run <= g && g < run + m) {
+                S.ibin = tid * per + q;
+                S.bex = run;
+            }
+            run += m;
+        }
+    }
+    if (tid == 0 && !(g < all)) S.bex = all;
+    __syncthreads();
+    const int b = S.ibin;
+    *above = S.bex;
+    __syncthreads();
+    return b;
+}
+
+// The full-row path on the bin histogram: one pass for the counts and masses of
+// every bin, then each crossing (top-k rank, top-p cut, draw) is found on the bins
+// and settled exactly among the elements of its one bin, gathered by a pass that
+// needs no weights.  Returns false (nothing decided) when a bin to be gathered
+// holds more than kGCap elements.
+template <int DT, bool VEC>
+FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pen, float rep,
+                         float pres, float freq, uint32_t k0, float M, int topk, float mp, float tp,
+                         double u, u128 sall, uint32_t* tk_out, uint32_t* tau_out, uint64_t* cut_out,
+                         u128* T_out, uint64_t* tok_out)
+{
+    const int tid = threadIdx.x;
+    for (int i = tid; i < kPassBins; i += kFinThreads) {
+        S.pc[i] = 0;
+        S.pm_lo[i] = 0;
+        S.pm_hi[i] = 0;
+    }
+    __syncthreads();
+    row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](uint64_t c) {
+        const int b = dbin_key(M, comp_k(c));
+        atomicAdd(&S.pc[b], 1u);
+        const u128 w = comp_weight(S, c);
+        const uint64_t lo = (uint64_t)w;
+        if (lo) {
+            const uint64_t old = atomicAdd((unsigned long long*)&S.pm_lo[b], (unsigned long long)lo);
+            const uint64_t hi = (uint64_t)(w >> 64) + ((old + lo < old) ? 1ull : 0ull);
+            if (hi) atomicAdd((unsigned long long*)&S.pm_hi[b], (unsigned long long)hi);
+        } else if ((uint64_t)(w >> 64)) {
+            atomicAdd((unsigned long long*)&S.pm_hi[b], (unsigned long long)(w >> 64));
+        }
+    });
+    int cur = -1, ncur = 0;   // the bin held in S.cand, its element count
+    auto gather = [&](int b) -> bool {
+        if (b == cur) return true;
+        if (S.pc[b] > (uint32_t)kGCap) return false;
+        if (tid == 0) S.n = 0;
+        __syncthreads();
+        row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](uint64_t c) {
+            if (dbin_key(M, comp_k(c)) == b) {
+                const uint32_t at = atomicAdd(&S.n, 1u);
+                if (at < (uint32_t)kGCap) S.cand[at] = c;
+            }
+        });
+        ncur = (int)S.n;
+        cur = b;
+        __syncthreads();
+        return true;
+    };
+
+    // top-k threshold: the element of rank topk - 1
+    uint32_t tk = 0;
+    if (topk > 0) {
+        u128 above;
+        const int b = dbin_pick<false>(S, kPassBins - 1, (u128)S.pc[kPassBins - 1], (u128)(topk - 1), &above);
+        if (b < 0 || !gather(b)) return false;
+        const SelResult r = lds_select<false>(S, ncur, Pred{0, 0, 0}, (u128)(topk - 1) - above);
+        if (!r.found) return false;
+        tk = comp_k(r.comp);
+    }
+    const uint32_t tmp = minp_key(M, mp);
+    const uint32_t tau = tk > tmp ? tk : tmp;
+
+    // survivors (key >= tau): whole bins before tau's bin, part of that bin
+    int bt = kPassBins - 1;
+    u128 lastt = bin_mass(S, kPassBins - 1);
+    u128 Sv = sall;
+    if (tau != 0) {
+        bt = dbin_key(M, tau);
+        if (!gather(bt)) return false;
+        u128 part = 0;
+        for (int i = tid; i < ncur; i += kFinThreads)
+            if (comp_k(S.cand[i]) >= tau) part += comp_weight(S, S.cand[i]);
+        for (int b = tid; b < bt; b += kFinThreads) part += bin_mass(S, b);
+        lastt = block_sum_u128<kFinThreads>(part, S.red128);
+        Sv = lastt;
+        // lastt so far holds the survivors' whole mass: take the bins before bt out
+        u128 before = 0;
+        for (int b = tid; b < bt; b += kFinThreads) before += bin_mass(S, b);
+        lastt -= block_sum_u128<kFinThreads>(before, S.red128);
+    }
+
+    // top-p cut among the survivors
+    uint64_t cut = 0;
+    u128 T = Sv;
+    int bc = bt;
+    u128 lastc = lastt;
+    if (tp < 1.0f) {
+        const u128 thr = ceil_mul_f32(tp, Sv);
+        u128 above;
+        const int b = dbin_pick<true>(S, bt, lastt, thr - 1, &above);
+        if (b < 0) {
+            T = above;                            // every survivor; no cut (Sv == 0)
+        } else {
+            if (!gather(b)) return false;
+            const SelResult r = lds_select<true>(S, ncur, Pred{tau, 0, 0}, thr - 1 - above);
+            if (!r.found) return false;
+            cut = r.comp;
+            T = above + r.excl + r.meas;
+            bc = b;
+            lastc = T - above;
+        }
+    }
+
+    // the draw among the kept tokens (the largest token when their mass is 0)
+    uint64_t tok = 0;
+    if (T == 0) {
+        u128 above;
+        const int b = dbin_pick<false>(S, kPassBins - 1, (u128)S.pc[kPassBins - 1], 0, &above);
+        if (b < 0 || !gather(b)) return false;
+        const SelResult r = lds_select<false>(S, ncur, Pred{0, 0, 0}, 0);
+        if (!r.found) return false;
+        tok = r.comp;
+    } else {
+        const u128 g = floor_mul_f64(u, T);
+        u128 above;
+        const int b = dbin_pick<true>(S, bc, lastc, g, &above);
+        if (b < 0 || !gather(b)) return false;
+        const SelResult r = lds_select<true>(S, ncur, Pred{tau, 0, cut}, g - above);
+        if (!r.found) return false;
+        tok = r.comp;
+    }
+    *tk_out = tk;
+    *tau_out = tau;
+    *cut_out = cut;
+    *T_out = T;
+    *tok_out = tok;
+    return true;
+}
+
 // Token 0 keeps its penalty iff the row is the widest of the batch (no pad entry
 // rewrites index 0 after it) and no id >= vocab first occurs after it
 // (sampler.py:148,156-157,174-175 with a sequential scatter).
@@ -419,23 +617,224 @@ FIE_DEV bool q1_keeps(FinSmem& S, const KParams& P, int row)
     return mine == wmax && !late;
 }
 
-// The row's candidates from every tile into S.cand as y-domain composites, token 0
-// last; one element per thread, all loads in flight together.
-FIE_DEV void load_candidates(FinSmem& S, const KParams& P, int row, int NT, int n, float s,
-                             uint32_t k0)
+// The row's candidates from every tile as y-domain composites, token 0 included:
+// those whose key exceeds `safe` (the complete region) into S.cand in any order,
+// at most kGCap of them.  Returns how many there are (possibly more than were
+// stored); S.cmax receives the largest composite of all n.
+FIE_DEV int load_candidates(FinSmem& S, const KParams& P, int row, int NT, int n, float s,
+                            uint32_t k0, uint32_t safe)
 {
-    for (int i = threadIdx.x; i < n - 1; i += kFinThreads) {
-        int lo = 0, hi = NT - 1;                 // tile t with coff[t] <= i < coff[t+1]
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (S.coff[mid] <= (uint32_t)i) lo = mid;
-            else hi = mid - 1;
-        }
-        const uint64_t xc = P.w.cand[((size_t)row * NT + lo) * kCapW + (i - S.coff[lo])];
-        S.cand[i] = comp_key(fkey(y_of_xkey(comp_k(xc), s)), comp_idx(xc));
-    }
-    if (threadIdx.x == 0) S.cand[n - 1] = comp_key(k0, 0);
+    if (threadIdx.x == 0) { S.n = 0; S.cmax = 0; }
     __syncthreads();
+    uint64_t best = 0;
+    for (int i = threadIdx.x; i < n; i += kFinThreads) {
+        uint64_t c;
+        if (i == n - 1) {
+            c = comp_key(k0, 0);
+        } else {
+            int lo = 0, hi = NT - 1;             // tile t with coff[t] <= i < coff[t+1]
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (S.coff[mid] <= (uint32_t)i) lo = mid;
+                else hi = mid - 1;
+            }
+            const uint64_t xc = P.w.cand[((size_t)row * NT + lo) * kCapW + (i - S.coff[lo])];
+            c = comp_key(fkey(y_of_xkey(comp_k(xc), s)), comp_idx(xc));
+        }
+        best = c > best ? c : best;
+        if (comp_k(c) > safe) {
+            const uint32_t at = atomicAdd(&S.n, 1u);
+            if (at < (uint32_t)kGCap) S.cand[at] = c;
+        }
+    }
+    best = wave_max_u64(best);
+    if ((threadIdx.x & 63) == 0 && best) atomicMax((unsigned long long*)&S.cmax, (unsigned long long)best);
+    __syncthreads();
+    const int m = (int)S.n;
+    __syncthreads();
+    return m;
+}
+
+// ---------------------------------------------------------------- sorted candidates
+constexpr int kSortMax = 8192;     // candidates sorted in LDS, at most
+
+// v of lane (lane ^ J): DPP moves inside rows of 16 lanes (quad permutes for 1 and
+// 2, row shifts by 4 and 8 selected by the lane's bit), a swizzle inside 32 lanes
+// for 16, a permute for 32.
+template <int J>
+FIE_DEV uint32_t lane_xor_u32(uint32_t v)
+{
+    const int lane = threadIdx.x & 63;
+    if constexpr (J == 1) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+    } else if constexpr (J == 2) {
+        return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+    } else if constexpr (J == 4 || J == 8) {
+        const uint32_t up = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x100 | J, 0xF, 0xF, false);
+        const uint32_t dn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x110 | J, 0xF, 0xF, false);
+        return (lane & J) ? dn : up;
+    } else if constexpr (J == 16) {
+        return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F);
+    } else {
+        return (uint32_t)__shfl_xor((int)v, 32, 64);
+    }
+}
+
+// One compare-exchange stage of stride J < 64 for block size k over a lane's two
+// elements e0 = base + lane, e1 = e0 + 64 (descending: the lower index of a pair
+// keeps the larger value where (index & k) == 0).
+template <int J>
+FIE_DEV void bitonic_stage(uint64_t& v0, uint64_t& v1, int e0, int e1, int k)
+{
+    const int lane = threadIdx.x & 63;
+    const uint32_t a = lane_xor_u32<J>((uint32_t)v0), b = lane_xor_u32<J>((uint32_t)(v0 >> 32));
+    const uint32_t c = lane_xor_u32<J>((uint32_t)v1), d = lane_xor_u32<J>((uint32_t)(v1 >> 32));
+    const uint64_t p0 = ((uint64_t)b << 32) | a, p1 = ((uint64_t)d << 32) | c;
+    const bool lower = (lane & J) == 0;
+    const bool max0 = lower == ((e0 & k) == 0), max1 = lower == ((e1 & k) == 0);
+    v0 = max0 ? (v0 > p0 ? v0 : p0) : (v0 < p0 ? v0 : p0);
+    v1 = max1 ? (v1 > p1 ? v1 : p1) : (v1 < p1 ? v1 : p1);
+}
+
+// One 128-element block of a descending bitonic sort inside one wave (lane holds
+// elements base + lane and base + 64 + lane): for each block size k in [k0, k1],
+// the compare-exchange stages of stride min(k / 2, 64) down to 1.  Stride 64 pairs
+// a lane's own two elements; smaller strides pair lanes (bitonic_stage).
+FIE_DEV void wave_bitonic(uint64_t* c, int base, int k0, int k1)
+{
+    const int lane = threadIdx.x & 63;
+    const int e0 = base + lane, e1 = base + 64 + lane;
+    uint64_t v0 = c[e0], v1 = c[e1];
+    for (int k = k0; k <= k1; k <<= 1) {
+        const int jm = k >> 1 < 64 ? k >> 1 : 64;
+        if (jm >= 64) {
+            const bool desc = (e0 & k) == 0;
+            const uint64_t hi = v0 > v1 ? v0 : v1, lo = v0 > v1 ? v1 : v0;
+            v0 = desc ? hi : lo;
+            v1 = desc ? lo : hi;
+        }
+        if (jm >= 32) bitonic_stage<32>(v0, v1, e0, e1, k);
+        if (jm >= 16) bitonic_stage<16>(v0, v1, e0, e1, k);
+        if (jm >= 8) bitonic_stage<8>(v0, v1, e0, e1, k);
+        if (jm >= 4) bitonic_stage<4>(v0, v1, e0, e1, k);
+        if (jm >= 2) bitonic_stage<2>(v0, v1, e0, e1, k);
+        bitonic_stage<1>(v0, v1, e0, e1, k);
+    }
+    c[e0] = v0;
+    c[e1] = v1;
+}
+
+// Sorts S.cand[0, n) descending (n <= kSortMax; composites are distinct), padding
+// with 0 to a power of two of at least 128.  Strides below 128 run inside waves;
+// only the larger strides of the merges take a barrier each.
+FIE_DEV void sort_desc(FinSmem& S, int n)
+{
+    const int tid = threadIdx.x, wave = tid >> 6;
+    int N = 128;
+    while (N < n) N <<= 1;
+    for (int i = n + tid; i < N; i += kFinThreads) S.cand[i] = 0;
+    __syncthreads();
+    for (int b = wave * 128; b < N; b += kFinThreads * 2) wave_bitonic(S.cand, b, 2, 128);
+    for (int k = 256; k <= N; k <<= 1) {
+        for (int j = k >> 1; j >= 128; j >>= 1) {
+            __syncthreads();
+            for (int i = tid; i < N / 2; i += kFinThreads) {
+                const int a0 = ((i & ~(j - 1)) << 1) | (i & (j - 1)), b0 = a0 + j;
+                const uint64_t x = S.cand[a0], y = S.cand[b0];
+                if ((x < y) == ((a0 & k) == 0)) {
+                    S.cand[a0] = y;
+                    S.cand[b0] = x;
+                }
+            }
+        }
+        __syncthreads();
+        for (int b = wave * 128; b < N; b += kFinThreads * 2) wave_bitonic(S.cand, b, k, k);
+    }
+    __syncthreads();
+}
+
+// Number of leading sorted candidates whose key satisfies key > t (strict) or
+// key >= t: a prefix, since the order is key-major.
+FIE_DEV int sorted_prefix(FinSmem& S, int n, uint32_t t, bool strict)
+{
+    if (threadIdx.x == 0) S.flag = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n; i += kFinThreads) {
+        const uint32_t k = comp_k(S.cand[i]);
+        const bool in = strict ? k > t : k >= t;
+        const bool next_in = i + 1 < n && (strict ? comp_k(S.cand[i + 1]) > t : comp_k(S.cand[i + 1]) >= t);
+        if (in && !next_in) S.flag = i + 1;
+    }
+    __syncthreads();
+    const int r = S.flag;
+    __syncthreads();
+    return r;
+}
+
+// Prefix masses (rule R1 weights) over the first m sorted candidates: thread t owns
+// the chunk [lo, hi) and knows the mass before it (base) and of it (sum).
+struct Chunks {
+    int lo, hi;
+    u128 base, sum;
+};
+
+FIE_DEV Chunks chunk_masses(FinSmem& S, int m)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = (m + kFinThreads - 1) / kFinThreads;
+    Chunks ch;
+    ch.lo = min(tid * E, m);
+    ch.hi = min(ch.lo + E, m);
+    ch.sum = 0;
+    for (int i = ch.lo; i < ch.hi; ++i) ch.sum += comp_weight(S, S.cand[i]);
+    const u128 incl = wave_incl_scan_u128(ch.sum);
+    if (lane == 63) S.red128[wave] = incl;
+    __syncthreads();
+    u128 before = 0;
+    for (int w = 0; w < wave; ++w) before += S.red128[w];
+    ch.base = before + incl - ch.sum;
+    __syncthreads();
+    return ch;
+}
+
+// The first sorted candidate i < lim whose inclusive prefix mass exceeds g, with
+// that prefix in *incl; -1 when the mass of the first lim candidates is <= g.
+FIE_DEV int chunk_find(FinSmem& S, const Chunks& ch, u128 g, int lim, u128* incl)
+{
+    if (threadIdx.x == 0) S.ibin = -1;
+    __syncthreads();
+    if (ch.lo < ch.hi && ch.base <= g && g < ch.base + ch.sum) {
+        u128 run = ch.base;
+        for (int i = ch.lo; i < ch.hi; ++i) {
+            run += comp_weight(S, S.cand[i]);
+            if (run > g) {
+                S.ibin = i;
+                S.bex = run;
+                break;
+            }
+        }
+    }
+    __syncthreads();
+    const int i = S.ibin;
+    *incl = S.bex;
+    __syncthreads();
+    return i >= 0 && i < lim ? i : -1;
+}
+
+// Mass of the first m sorted candidates (m <= the chunked length).
+FIE_DEV u128 chunk_prefix(FinSmem& S, const Chunks& ch, int m)
+{
+    if (threadIdx.x == 0) S.bme = 0;
+    __syncthreads();
+    if (m > 0 && ch.lo <= m - 1 && m - 1 < ch.hi) {
+        u128 run = ch.base;
+        for (int i = ch.lo; i < m; ++i) run += comp_weight(S, S.cand[i]);
+        S.bme = run;
+    }
+    __syncthreads();
+    const u128 r = S.bme;
+    __syncthreads();
+    return r;
 }
 
 // ---------------------------------------------------------------- k_finish
@@ -459,11 +858,13 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
     int32_t status = 0;
     if (pen && P.w.bad[row] && !a.hist_invalid) status |= FIE_ROW_UNCOUNTED_IDS;
 
+    FIE_MARK(0);
     // Tile maxima (x keys) and the row maximum.
     if (tid < NT) S.tmc[tid] = P.w.maxc[(size_t)row * NT + tid];
     __syncthreads();
     const uint64_t xm = block_max_u64<kFinThreads>(tid < NT ? S.tmc[tid] : 0ull, S.red64);
 
+    FIE_MARK(1);
     // Token 0 (a tile of its own).
     const float x0 = P.w.tok0x[row];
     const uint32_t c0 = pen ? P.w.tok0c[row] : 0u;
@@ -494,6 +895,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
     }
     __syncthreads();
 
+    FIE_MARK(2);
     // Whole-row mass (rule R1): sum over tiles of C_t * (tile sum of weights).
     u128 sall = 0;
     if (need_mass) {
@@ -503,6 +905,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
         sall = block_sum_u128<kFinThreads>(part, S.red128);
     }
 
+    FIE_MARK(3);
     int64_t token = -1;
     uint64_t tok_comp = 0;   // y-domain composite of the chosen token
     uint32_t tau = 0;
@@ -520,10 +923,12 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
         T = comp_weight(S, best);
     }
 
-    // Candidates as y-domain composites, and the safety key: every token whose
-    // scaled key exceeds `safe` is among them.
-    int n = 0;
+    // Candidates as y-domain composites, sorted, and the safety key: every token
+    // whose scaled key exceeds `safe` is among them.
+    int n = 0, nv = 0;       // candidates, and those above the safety key (sorted)
     uint32_t safe = 0;
+    uint64_t cmax = 0;       // the largest candidate composite
+    bool sorted = false;
     const bool need_cand = !greedy || lp > 0;
     if (need_cand) {
         // per-tile counts and bounds: one load per thread, a block prefix sum
@@ -541,63 +946,78 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
         if (kx <= 1u || kx <= kKeyNegInf) safe = 0;
         else if (kx > kKeyPosInf) safe = 0xFFFFFFFFu;
         else safe = fkey(y_of_xkey(kx, s));
-        if (n > kGCap) deep = true;
-        else load_candidates(S, P, row, NT, n, s, k0);
+        // only the complete region is ever used: candidates at or below the safety
+        // key are dropped before sorting (S.cmax keeps the largest of all)
+        nv = load_candidates(S, P, row, NT, n, s, k0, safe);
+        cmax = S.cmax;
+        if (nv > kSortMax) {
+            deep = true;
+        } else {
+            sort_desc(S, nv);
+            sorted = true;
+        }
     }
 
-    // Sampled rows on the candidates: top-k, min-p, S, top-p cut, draw.
+    // Sampled rows on the sorted candidates: top-k, min-p, S, top-p cut, draw.
+    FIE_MARK(4);
     if (!greedy && !deep) {
-        const Pred all{0, 0, 0};
         uint32_t tk = 0;
         if (topk > 0) {
-            if (n < topk) deep = true;
-            else {
-                const SelResult r = lds_select<false>(S, n, all, (u128)(topk - 1));
-                tk = comp_k(r.comp);
-                if (!r.found || tk <= safe) deep = true;
-            }
+            // the top-k threshold lies in the complete region iff it holds topk
+            if (nv < topk) deep = true;
+            else tk = comp_k(S.cand[topk - 1]);
         }
         const uint32_t tmp = minp_key(M, mp);
         tau = tk > tmp ? tk : tmp;
         if (!deep && tau != 0 && tau <= safe) deep = true;
+        FIE_MARK(5);
         if (!deep) {
-            u128 Sv = sall;
-            if (tau != 0) {
-                u128 part = 0;
-                for (int i = tid; i < n; i += kFinThreads)
-                    if (comp_k(S.cand[i]) >= tau) part += comp_weight(S, S.cand[i]);
-                Sv = block_sum_u128<kFinThreads>(part, S.red128);
-            }
-            const Pred surv{tau, safe, 0};
+            // survivors (key >= tau) and the complete region (key > safe) are
+            // prefixes of the sorted candidates; with tau != 0 the survivors lie in it
+            const int ns = tau != 0 ? sorted_prefix(S, nv, tau, false) : nv;
+            const Chunks ch = chunk_masses(S, nv);
+            const u128 Sv = tau != 0 ? chunk_prefix(S, ch, ns) : sall;
+            FIE_MARK(6);
+            int lim = ns;
             if (tp < 1.0f) {
                 const u128 thr = ceil_mul_f32(tp, Sv);
-                const SelResult r = lds_select<true>(S, n, surv, thr - 1);
-                if (!r.found) deep = true;
-                else { cut = r.comp; T = r.excl + r.meas; }
+                u128 incl;
+                const int i = chunk_find(S, ch, thr - 1, lim, &incl);
+                if (i < 0) deep = true;
+                else { cut = S.cand[i]; T = incl; lim = i + 1; }
             } else {
                 T = Sv;
             }
+            FIE_MARK(7);
             if (!deep) {
                 if (T == 0) {
-                    const SelResult r = lds_select<false>(S, n, all, 0);
-                    token = comp_idx(r.comp);
-                    tok_comp = r.comp;
+                    token = comp_idx(cmax);
+                    tok_comp = cmax;
                 } else {
                     const u128 g = floor_mul_f64(a.uniform[row], T);
-                    const SelResult r = lds_select<true>(S, n, Pred{tau, safe, cut}, g);
-                    if (!r.found) deep = true;
-                    else { token = comp_idx(r.comp); tok_comp = r.comp; }
+                    u128 incl;
+                    const int i = chunk_find(S, ch, g, lim, &incl);
+                    if (i < 0) deep = true;
+                    else { token = comp_idx(S.cand[i]); tok_comp = S.cand[i]; }
                 }
             }
         }
+        FIE_MARK(8);
         if (!deep && a.tk_key && tid == 0) a.tk_key[row] = tk;
     }
 
+    FIE_MARK(9);
     // Full-row path for sampled rows the candidates could not settle.
     if (!greedy && deep) {
         status |= FIE_ROW_EXACT_PATH;
         cut = 0;
         uint32_t tk = 0;
+        const bool binned = binned_deep<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, M, topk, mp, tp,
+                                                 a.uniform[row], sall, &tk, &tau, &cut, &T, &tok_comp);
+        if (!binned) {
+        // radix levels over the composite, re-reading the row per level
+        cut = 0;
+        tk = 0;
         if (topk > 0) {
             const SelResult r = row_select<DT, VEC, false>(S, P, row, s, pen, rep, pres, freq, k0,
                                                            Pred{0, 0, 0}, (u128)(topk - 1), false);
@@ -632,12 +1052,21 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
                                                           Pred{tau, 0, cut}, g, l1);
             tok_comp = r.comp;
         }
+        }
         token = comp_idx(tok_comp);
         if (a.tk_key && tid == 0) a.tk_key[row] = tk;
         // the LDS candidates were overwritten: reload them for the logprobs below
-        if (lp > 0 && n <= kGCap) load_candidates(S, P, row, NT, n, s, k0);
+        sorted = false;
+        if (lp > 0 && n > 0) {
+            nv = load_candidates(S, P, row, NT, n, s, k0, safe);
+            if (nv <= kSortMax) {
+                sort_desc(S, nv);
+                sorted = true;
+            }
+        }
     }
 
+    FIE_MARK(10);
     // Logprobs (sampler.py:262-291, rule R7): chosen token, then the row's best L,
     // all from the penalised, scaled distribution before filtering.
     if (lp >= 0) {
@@ -645,44 +1074,38 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
             a.chosen_logprob[row] = (float)(((double)key_to_float(comp_k(tok_comp)) - (double)M) - lse);
         const int L = lp < a.lp_cols ? lp : a.lp_cols;
         if (L > 0) {
-            bool ok = n >= L && n <= kGCap;
-            SelResult r{0, 0, 0, 0};
-            if (ok) {
-                r = lds_select<false>(S, n, Pred{0, 0, 0}, (u128)(L - 1));
-                ok = r.found && comp_k(r.comp) > safe;
-            }
-            if (!ok) {
-                r = row_select<DT, VEC, false>(S, P, row, s, pen, rep, pres, freq, k0,
-                                               Pred{0, 0, 0}, (u128)(L - 1), false);
-                n = pass_gather<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0,
-                                         Pred{0, 0, r.comp}, 64, 0);
-            }
-            // the L composites >= r.comp (exactly L of them), then sorted by one thread
-            if (tid == 0) S.bcnt = 0;
-            __syncthreads();
-            for (int i = tid; i < n; i += kFinThreads) {
-                const uint64_t c = S.cand[i];
-                if (c >= r.comp) {
-                    const uint32_t at = atomicAdd(&S.bcnt, 1u);
-                    if (at < 32) ((uint64_t*)S.hm_lo)[at] = c;
-                }
-            }
-            __syncthreads();
-            if (tid == 0) {
-                const int m = (int)(S.bcnt < 32 ? S.bcnt : 32);
-                uint64_t* top = (uint64_t*)S.hm_lo;
-                for (int i = 1; i < m; ++i) {
-                    const uint64_t c = top[i];
-                    int j = i;
-                    while (j > 0 && top[j - 1] < c) { top[j] = top[j - 1]; --j; }
-                    top[j] = c;
-                }
-                for (int j = 0; j < a.lp_cols; ++j) {
+            if (sorted && nv >= L) {
+                // the first L sorted candidates
+                for (int j = tid; j < a.lp_cols; j += kFinThreads) {
                     const size_t o = (size_t)row * a.lp_cols + j;
-                    const bool have = j < m && j < L;
-                    if (a.top_ids) a.top_ids[o] = have ? (int64_t)comp_idx(top[j]) : -1;
+                    const bool have = j < L;
+                    const uint64_t c = have ? S.cand[j] : 0ull;
+                    if (a.top_ids) a.top_ids[o] = have ? (int64_t)comp_idx(c) : -1;
                     if (a.top_logprobs)
-                        a.top_logprobs[o] = have ? (float)(((double)key_to_float(comp_k(top[j])) - (double)M) - lse) : 0.0f;
+                        a.top_logprobs[o] = have ? (float)(((double)key_to_float(comp_k(c)) - (double)M) - lse) : 0.0f;
+                }
+            } else {
+                // the L-th largest composite over the row, the L composites >= it
+                // gathered, then sorted by one thread
+                const SelResult r = row_select<DT, VEC, false>(S, P, row, s, pen, rep, pres, freq, k0,
+                                                               Pred{0, 0, 0}, (u128)(L - 1), false);
+                n = pass_gather<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, Pred{0, 0, r.comp}, 64, 0);
+                if (tid == 0) {
+                    const int m = n < 32 ? n : 32;
+                    uint64_t* top = S.cand;
+                    for (int i = 1; i < m; ++i) {
+                        const uint64_t c = top[i];
+                        int j = i;
+                        while (j > 0 && top[j - 1] < c) { top[j] = top[j - 1]; --j; }
+                        top[j] = c;
+                    }
+                    for (int j = 0; j < a.lp_cols; ++j) {
+                        const size_t o = (size_t)row * a.lp_cols + j;
+                        const bool have = j < m && j < L;
+                        if (a.top_ids) a.top_ids[o] = have ? (int64_t)comp_idx(top[j]) : -1;
+                        if (a.top_logprobs)
+                            a.top_logprobs[o] = have ? (float)(((double)key_to_float(comp_k(top[j])) - (double)M) - lse) : 0.0f;
+                    }
                 }
             }
         } else if (tid == 0) {
@@ -694,6 +1117,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
         }
     }
 
+    FIE_MARK(11);
     if (tid == 0) {
         a.tokens[row] = token;
         if (a.status) a.status[row] = status;

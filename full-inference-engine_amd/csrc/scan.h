@@ -517,10 +517,10 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
                 const uint32_t idx = (uint32_t)(q * 64 + lane);
                 sk[q] = idx < E ? comp_k(st[idx]) : 0u;
             }
-            // the floor fixed the top 12 bits unless it stayed at 0 (fewer than c
-            // groups in the tile, all of them staged)
-            const uint32_t K = floor_key ? ballot_select(sk, c, floor_key & 0xFFF00000u, 19, 0)
-                                         : ballot_select(sk, c, 0u, 31, 0);
+            // the c-th largest staged key, searched over all 32 bits: the floor
+            // bounds it from below only (a group may hold several tokens above
+            // the floor's bucket, so the answer can lie above that bucket)
+            const uint32_t K = ballot_select(sk, c, 0u, 31, 0);
             uint32_t ge = 0;
 #pragma unroll
             for (int q = 0; q < SPL; ++q) ge += popc64(__ballot(sk[q] >= K));
@@ -539,8 +539,12 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
             nout += popc64(bal);
         }
         if (lane == 0) {
-            P.w.ncand[slot] = nout;
-            P.w.bound[slot] = bound;
+            // more than kCapW at or above the bound cannot happen (the bound is the
+            // c-th largest staged key, c <= kCapW); should it, the tile reports
+            // itself incomplete and the row takes the full-row path
+            const bool over = nout > (uint32_t)kCapW;
+            P.w.ncand[slot] = over ? 0u : nout;
+            P.w.bound[slot] = over ? 0xFFFFFFFFu : bound;
         }
     }
 }
