@@ -10,6 +10,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "finish.h"
 #include "fie_sampler.h"
 
@@ -294,6 +296,34 @@ static int prepare(const fie_sampler_args* args, const fie_workspace* ws, KParam
     return ws_of(ws, args->rows, args->vocab, &P->w);
 }
 
+// ---------------------------------------------------------------- static scratch
+// The workspace of fie_sampler_sample_noalloc: a device array per GPU, reached
+// through the address hipGetSymbolAddress returns on that device (the array's
+// name is a host-side stand-in, never a device address).
+static __device__ __align__(256) unsigned char scratch[FIE_SCRATCH_BYTES];
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch[kMaxDevices];
+
+static int scratch_of(void** out)
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess) return fail(FIE_E_LAUNCH, "hipGetDevice failed");
+    if (dev < 0 || dev >= kMaxDevices) return fail(FIE_E_ARG, "device ordinal out of range [0, 64)");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !p) {
+            snprintf(g_err, sizeof g_err, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+            return FIE_E_LAUNCH;
+        }
+        g_scratch[dev] = p;
+    }
+    *out = g_scratch[dev];
+    return FIE_OK;
+}
+
 }  // namespace fie
 
 using namespace fie;
@@ -390,5 +420,20 @@ int fie_sampler_cexp(const float* in, float* out, int64_t n, void* stream)
 }
 
 const char* fie_sampler_last_error(void) { return g_err; }
+
+int fie_sampler_sample_noalloc(const fie_sampler_args* args, void* stream)
+{
+    int rc = check_args(args);
+    if (rc != FIE_OK || args->rows == 0) return rc;
+    Layout L;
+    if (!layout_of(args->rows, args->vocab, &L)) return fail(FIE_E_ARG, "sizes out of range");
+    if (L.total > FIE_SCRATCH_BYTES)
+        return fail(FIE_E_WORKSPACE, "rows x vocab need more than the 64 MiB static scratch");
+    void* p = nullptr;
+    rc = scratch_of(&p);
+    if (rc != FIE_OK) return rc;
+    const fie_workspace ws{p, FIE_SCRATCH_BYTES, args->rows, args->vocab};
+    return fie_sampler_sample(args, &ws, stream);
+}
 
 }  // extern "C"

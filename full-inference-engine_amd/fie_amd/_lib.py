@@ -54,7 +54,9 @@ class Workspace(ctypes.Structure):
 EXPORTS = (
     "fie_sampler_workspace_size", "fie_sampler_sample", "fie_sampler_stage",
     "fie_sampler_argmax", "fie_sampler_kept", "fie_sampler_cexp", "fie_sampler_last_error",
+    "fie_sampler_sample_noalloc",
 )
+SCRATCH_BYTES = 64 << 20
 
 _lib = None
 
@@ -92,6 +94,7 @@ def bind(lib) -> None:
     lib.fie_sampler_kept.argtypes = [
         ctypes.POINTER(SamplerArgs), _vp, _vp, ctypes.POINTER(Workspace), _vp]
     lib.fie_sampler_cexp.argtypes = [_vp, _vp, ctypes.c_int64, _vp]
+    lib.fie_sampler_sample_noalloc.argtypes = [ctypes.POINTER(SamplerArgs), _vp]
     lib.fie_sampler_last_error.restype = ctypes.c_char_p
     for name in EXPORTS:
         if name not in ("fie_sampler_workspace_size", "fie_sampler_last_error"):

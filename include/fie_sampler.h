@@ -154,6 +154,17 @@ int fie_sampler_cexp(const float* in, float* out, int64_t n, void* stream);
 /* Message of the last failing call on this thread (static storage). */
 const char* fie_sampler_last_error(void);
 
+/* fie_sampler_sample without a caller workspace and without any allocation: the
+ * kernels use a static device array of FIE_SCRATCH_BYTES (64 MiB), resolved once
+ * per device on the first call there and held by each device until the process
+ * ends.  No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops).  Returns
+ * FIE_E_WORKSPACE when fie_sampler_workspace_size(rows, vocab) exceeds the array.
+ * Calls that overlap on one device share the array and race; calls on one stream,
+ * or otherwise ordered, are safe. */
+#define FIE_SCRATCH_BYTES ((size_t)64 << 20)
+int fie_sampler_sample_noalloc(const fie_sampler_args* args, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
