@@ -1,0 +1,277 @@
+"""CPU tests of the host side: the parameter type, history packing, per-request
+uniforms, logprob assembly, and the C-ABI's exports and argument errors (no
+kernel runs; the library loads without a GPU).
+
+The reference behaviour restated here is engine/runtime/sampling.py:19-97 and
+engine/batching/sampler.py:32-117,262-291 (read, not run).
+"""
+
+import ctypes
+import os
+import re
+
+import numpy as np
+import pytest
+
+from fie_amd import _lib
+from fie_amd.batching.sampler import BatchedSampler, SampleResult, pack_history, resolve_params
+from fie_amd.kernel import FLAG_GREEDY, FLAG_PENALTY
+from fie_amd.runtime.sampling import GREEDY, SamplingParams
+
+HEADER = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "include", "fie_sampler.h")
+
+
+# ---------------------------------------------------------------- SamplingParams
+def test_defaults_are_plain_greedy():
+    p = SamplingParams()
+    assert (p.temperature, p.top_p, p.top_k, p.min_p) == (0.0, 1.0, 0, 0.0)
+    assert (p.repetition_penalty, p.presence_penalty, p.frequency_penalty) == (1.0, 0.0, 0.0)
+    assert p.greedy and not p.has_penalties and p.deterministic and p.can_reuse_cached_prediction
+    assert GREEDY == p
+    assert SamplingParams(stop_token_ids=[3, 3, 5]).stop_token_ids == frozenset({3, 5})
+
+
+@pytest.mark.parametrize("kwargs, message", [
+    (dict(temperature=-0.1), "temperature must be in [0, 2]"),
+    (dict(temperature=2.5), "temperature must be in [0, 2]"),
+    (dict(top_p=0.0), "top_p must be in (0, 1]"),
+    (dict(top_p=1.5), "top_p must be in (0, 1]"),
+    (dict(top_k=-1), "top_k must be non-negative (0 disables it)"),
+    (dict(min_p=1.5), "min_p must be in [0, 1]"),
+    (dict(repetition_penalty=0.0), "repetition_penalty must be in (0, 2]"),
+    (dict(repetition_penalty=2.5), "repetition_penalty must be in (0, 2]"),
+    (dict(presence_penalty=-3.0), "presence_penalty must be in [-2, 2]"),
+    (dict(frequency_penalty=2.5), "frequency_penalty must be in [-2, 2]"),
+    (dict(logprobs=21), "logprobs must be in [0, 20]"),
+    (dict(seed=-1), "seed must be a non-negative 63-bit integer"),
+    (dict(seed=2**63), "seed must be a non-negative 63-bit integer"),
+])
+def test_validation_matches_the_reference_messages(kwargs, message):
+    """sampling.py:50-69: the same ranges, each failure a ValueError with its text."""
+    with pytest.raises(ValueError) as e:
+        SamplingParams(**kwargs)
+    assert str(e.value) == message
+
+
+def test_predicates():
+    """sampling.py:71-94."""
+    assert SamplingParams(temperature=0.8, top_k=1).greedy
+    assert not SamplingParams(temperature=0.8).greedy
+    assert SamplingParams(temperature=0.8, seed=3).deterministic
+    assert not SamplingParams(temperature=0.8).deterministic
+    assert SamplingParams(presence_penalty=0.1).has_penalties
+    assert not SamplingParams(presence_penalty=0.1).can_reuse_cached_prediction
+    assert not SamplingParams(logprobs=2).can_reuse_cached_prediction
+
+
+# ---------------------------------------------------------------- host packing
+def _naive_pack(contexts, include, vocab):
+    """The history CSR and the Q1 flags by direct definition: first occurrences in
+    order, ids >= vocab counted distinct, bit 30 when one first occurs after 0."""
+    offs, ids, invalid = [0], [], []
+    for c, inc in zip(contexts, include):
+        c = list(c) if inc else []
+        ids.extend(c)
+        offs.append(len(ids))
+        big_first = {}
+        for pos, t in enumerate(c):
+            if t >= vocab and t not in big_first:
+                big_first[t] = pos
+        v = len(big_first)
+        if 0 in c and any(pos > c.index(0) for pos in big_first.values()):
+            v |= 1 << 30
+        invalid.append(v)
+    return np.array(offs), np.array(ids, dtype=np.int32), np.array(invalid, dtype=np.int32)
+
+
+def test_pack_history_matches_its_definition():
+    rng = np.random.default_rng(3)
+    vocab = 50
+    for _ in range(40):
+        rows = int(rng.integers(1, 7))
+        contexts = [list(rng.integers(0, vocab + 4, size=int(rng.integers(0, 12)))) for _ in range(rows)]
+        include = rng.random(rows) < 0.7
+        offs, ids, invalid, longest = pack_history(contexts, include, vocab)
+        w_offs, w_ids, w_inv = _naive_pack(contexts, include, vocab)
+        np.testing.assert_array_equal(offs, w_offs)
+        np.testing.assert_array_equal(ids, w_ids)
+        np.testing.assert_array_equal(invalid if invalid is not None else np.zeros(rows, np.int32), w_inv)
+        assert longest == max(np.diff(w_offs))
+
+
+def test_pack_history_rejects_negative_ids():
+    with pytest.raises(ValueError):
+        pack_history([[1, -2]], np.array([True]), 10)
+
+
+def test_resolve_params_follows_the_reference_row_rules():
+    """sampler.py:109,182-192: greedy rows are unscaled and unfiltered; top_k >= vocab,
+    top_p == 1 and min_p == 0 are off; penalties apply only with contexts."""
+    vocab = 100
+    params = [SamplingParams(),
+              SamplingParams(temperature=0.5, top_k=150, top_p=0.9, min_p=0.1),
+              SamplingParams(temperature=0.7, top_k=1, top_p=0.5),
+              SamplingParams(temperature=1.2, repetition_penalty=1.3, logprobs=3)]
+    hp = resolve_params(params, vocab, np.zeros(4), [[1, 2], [3], [4], [5, 5, 7]])
+    np.testing.assert_array_equal(hp.scale, np.float32([1.0, 0.5, 1.0, 1.2]))
+    np.testing.assert_array_equal(hp.top_k, [0, 0, 0, 0])
+    np.testing.assert_array_equal(hp.top_p, np.float32([1.0, 0.9, 1.0, 1.0]))
+    np.testing.assert_array_equal(hp.min_p, np.float32([0.0, 0.1, 0.0, 0.0]))
+    np.testing.assert_array_equal(hp.flags, [FLAG_GREEDY, 0, FLAG_GREEDY, FLAG_PENALTY])
+    np.testing.assert_array_equal(hp.logprobs, [-1, -1, -1, 3])
+    assert hp.apply_penalties
+    np.testing.assert_array_equal(hp.hist_off, [0, 0, 0, 0, 3])    # only the penalised row
+    np.testing.assert_array_equal(hp.hist_ids, [5, 5, 7])
+    assert not resolve_params(params, vocab, np.zeros(4), None).apply_penalties
+
+
+# ---------------------------------------------------------------- the adapter's calls
+class _NoKernels(BatchedSampler):
+    """BatchedSampler with its host state only (the constructor's device setup is
+    skipped): exercises validation, uniforms and logprob assembly on the CPU."""
+
+    def __init__(self, generator_seed=None, max_generators=1024):
+        from collections import OrderedDict
+        self._generator = np.random.Generator(np.random.PCG64(generator_seed))
+        self._seeded = OrderedDict()
+        self._max_generators = max_generators
+
+
+def test_sample_validation_errors():
+    """sampler.py:89-97."""
+    import torch
+    s = _NoKernels()
+    x = torch.zeros(2, 5)
+    with pytest.raises(ValueError):
+        s.sample(torch.zeros(5), [GREEDY])
+    with pytest.raises(ValueError):
+        s.sample(x, [GREEDY])
+    with pytest.raises(ValueError):
+        s.sample(x, [GREEDY] * 2, context_tokens=[[1]])
+    with pytest.raises(ValueError):
+        s.sample(x, [GREEDY] * 2, request_ids=["a"])
+    assert s.sample(torch.zeros(0, 5), []) == SampleResult([], {})
+
+
+def test_seeded_rows_are_reproducible_per_request():
+    """sampler.py:58-73: a seeded request draws from its own generator, keyed by
+    request id (two requests with one seed do not share a stream), unaffected by
+    the rest of the batch; forget() starts it over."""
+    p = SamplingParams(temperature=1.0, seed=7)
+    q = SamplingParams(temperature=1.0)
+    a = _NoKernels(generator_seed=1)
+    u1 = a._uniforms([p, q, p], ["r1", "x", "r2"])
+    assert u1[0] == u1[2]                       # same seed, different requests
+    b = _NoKernels(generator_seed=99)
+    u2 = b._uniforms([q, q, p], ["y", "z", "r1"])
+    assert u2[2] == u1[0]                       # batch-independent
+    assert a._uniforms([p], ["r1"])[0] != u1[0]  # the stream advances
+    a.forget(["r1"])
+    assert a._uniforms([p], ["r1"])[0] == u1[0]  # and restarts after forget
+    assert a._uniforms([GREEDY], ["g"])[0] == 0.0
+
+
+def test_generator_cache_is_capped():
+    s = _NoKernels(max_generators=3)
+    p = SamplingParams(temperature=1.0, seed=1)
+    s._uniforms([p] * 5, [f"r{i}" for i in range(5)])
+    assert list(s._seeded) == ["r2", "r3", "r4"]
+
+
+def test_logprob_entries_follow_the_reference_layout():
+    """sampler.py:282-290: (chosen, lp) first, then the best alternatives other than
+    the chosen token, at most count + 1 entries."""
+    params = [SamplingParams(logprobs=2), GREEDY, SamplingParams(temperature=1.0, logprobs=0)]
+    out = {"chosen_lp": np.float32([-0.5, 0.0, -1.5]),
+           "top_ids": np.array([[4, 9, 1], [0, 0, 0], [-1, -1, -1]]),
+           "top_lp": np.float32([[-0.5, -1.0, -2.0], [0, 0, 0], [0, 0, 0]])}
+    got = BatchedSampler._logprobs(params, [4, 3, 8], out)
+    assert got == {0: [(4, -0.5), (9, -1.0)], 2: [(8, -1.5)]}
+
+
+# ---------------------------------------------------------------- the C-ABI
+def _declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(fie_\w+)\s*\(", text, re.M)))
+
+
+def test_library_exports_every_declared_function():
+    lib = _lib.load()
+    declared = _declared_functions()
+    assert len(declared) >= 8
+    assert set(declared) == set(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+
+
+def test_workspace_size():
+    lib = _lib.load()
+    assert lib.fie_sampler_workspace_size(256, 151936) > 256 * 151936 // 2048 * 64 * 8
+    assert lib.fie_sampler_workspace_size(1, 0) == 0
+    assert lib.fie_sampler_workspace_size(1, _lib.MAX_VOCAB + 1) == 0
+    assert lib.fie_sampler_workspace_size(1024, 151936) <= _lib.SCRATCH_BYTES
+
+
+def _args(**kw):
+    a = _lib.SamplerArgs()
+    a.dtype, a.rows, a.vocab, a.row_stride, a.lp_cols = _lib.FIE_F32, 2, 100, 100, 0
+    for f in ("logits", "tokens", "scale", "top_k", "top_p", "min_p", "flags", "uniform"):
+        setattr(a, f, 256)           # never dereferenced: every case fails its checks first
+    for k, v in kw.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("kw, code, text", [
+    (dict(dtype=7), _lib.FIE_E_ARG, b"dtype"),
+    (dict(rows=-1), _lib.FIE_E_ARG, b"rows"),
+    (dict(vocab=0), _lib.FIE_E_ARG, b"vocab"),
+    (dict(row_stride=50), _lib.FIE_E_ARG, b"row_stride"),
+    (dict(lp_cols=21), _lib.FIE_E_ARG, b"lp_cols"),
+    (dict(logits=None), _lib.FIE_E_ARG, b"NULL"),
+    (dict(apply_penalties=1), _lib.FIE_E_ARG, b"penalt"),
+])
+def test_sample_rejects_bad_arguments(kw, code, text):
+    lib = _lib.load()
+    a = _args(**kw)
+    ws = _lib.Workspace(256, 1 << 20, 2, 100)
+    assert lib.fie_sampler_sample(ctypes.byref(a), ctypes.byref(ws), None) == code
+    assert text in lib.fie_sampler_last_error()
+
+
+def test_sample_rejects_bad_workspaces():
+    lib = _lib.load()
+    a = _args()
+    need = lib.fie_sampler_workspace_size(2, 100)
+    cases = [(_lib.Workspace(None, need, 2, 100), b"missing"),
+             (_lib.Workspace(256 + 8, need, 2, 100), b"aligned"),
+             (_lib.Workspace(256, need, 1, 100), b"fewer rows"),
+             (_lib.Workspace(256, need - 1, 2, 100), b"too small")]
+    for ws, text in cases:
+        assert lib.fie_sampler_sample(ctypes.byref(a), ctypes.byref(ws), None) == _lib.FIE_E_WORKSPACE
+        assert text in lib.fie_sampler_last_error()
+    assert lib.fie_sampler_sample(None, None, None) == _lib.FIE_E_ARG
+    assert lib.fie_sampler_stage(ctypes.byref(a), ctypes.byref(cases[0][0]), 5, None) == _lib.FIE_E_ARG
+
+
+def test_zero_rows_is_a_no_op():
+    lib = _lib.load()
+    a = _args(rows=0)
+    assert lib.fie_sampler_sample(ctypes.byref(a), None, None) == _lib.FIE_OK
+    assert lib.fie_sampler_sample_noalloc(ctypes.byref(a), None) == _lib.FIE_OK
+
+
+def test_noalloc_rejects_shapes_beyond_its_array_before_any_device_call():
+    lib = _lib.load()
+    a = _args(rows=4096, vocab=151936, row_stride=151936)
+    assert lib.fie_sampler_sample_noalloc(ctypes.byref(a), None) == _lib.FIE_E_WORKSPACE
+    assert b"static scratch" in lib.fie_sampler_last_error()
+
+
+def test_argmax_and_cexp_argument_errors():
+    lib = _lib.load()
+    assert lib.fie_sampler_argmax(None, 9, 1, 10, 10, None, None, None) == _lib.FIE_E_ARG
+    assert lib.fie_sampler_argmax(None, 0, 1, 10, 5, None, None, None) == _lib.FIE_E_ARG
+    assert lib.fie_sampler_argmax(None, 0, 1, 10, 10, None, None, None) == _lib.FIE_E_ARG
+    assert lib.fie_sampler_cexp(None, None, -1, None) == _lib.FIE_E_ARG
+    assert lib.fie_sampler_cexp(None, None, 0, None) == _lib.FIE_OK
