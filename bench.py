@@ -29,7 +29,7 @@ sys.path.insert(0, os.path.join(_REPO, "full-inference-engine_amd"))
 
 METRIC = "rows/s + µs per sampler step at B=256,V=152k; % of HBM roofline"
 HBM_PEAK_GBS = 8000.0
-STAGES = ("k_scan", "k_finish")
+STAGES = ("k_prep", "k_scan", "k_finish")   # fie_sampler_stage 0, 1, 2
 
 
 def parse():
@@ -109,18 +109,23 @@ def time_config(config: int, steps: int, warmup: int, ring_mb: int, dev):
     torch.cuda.synchronize()
     ms_per_step = t0.elapsed_time(t1) / steps
 
-    # Per-kernel durations: the same launches, one HIP event between kernels, all on
-    # the stream the kernels run on.
+    # Per-kernel durations: each kernel alone, launched `steps` times back to back on
+    # the kernels' stream between one pair of HIP events (a pair per launch would add
+    # the event's own few microseconds to every kernel).  Each stage reads what the
+    # previous stages left in the workspace, so they run in chain order.
     nst = len(STAGES)
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(nst + 1)] for _ in range(steps)]
-    for i in range(steps):
-        ev[i][0].record(stream)
-        for s in range(nst):
+    stage_ms = []
+    for s in range(nst):
+        fs.launch_stage(args[0], s)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(steps):
             fs.launch_stage(args[i % nbuf], s)
-            ev[i][s + 1].record(stream)
-    torch.cuda.synchronize()
-    stage_ms = [statistics.median(ev[i][s].elapsed_time(ev[i][s + 1]) for i in range(steps))
-                for s in range(nst)]
+        e1.record(stream)
+        torch.cuda.synchronize()
+        stage_ms.append(e0.elapsed_time(e1) / steps)
+    if not hp.apply_penalties:
+        stage_ms[0] = 0.0                                   # k_prep is not launched
 
     # One checked step: status bits of the rows (the exact path is informational).
     buf.download(stream)

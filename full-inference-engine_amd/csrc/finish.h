@@ -202,7 +202,9 @@ FIE_DEV void recount(FinSmem& S, const fie_sampler_args& a, int row, int lo, int
 }
 
 // Visit every token of the row once, re-reading it from memory: f(comp) with the
-// y-domain composite of each token (token 0 with its settled value y0).
+// y-domain composite of each token (token 0 with its settled value y0).  The next
+// chunk's loads are in flight while a chunk is processed; a penalised row counts
+// its chunk's history first, so those loads never wait behind the prefetch.
 template <int DT, bool VEC, class F>
 FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, float rep,
                       float pres, float freq, uint32_t k0, F&& f)
@@ -212,13 +214,19 @@ FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, 
     const fie_sampler_args& a = P.a;
     const int V = a.vocab, tid = threadIdx.x;
     const char* rowp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * SZ;
+    const bool mark = s != 1.0f && s >= 0x1p-30f && s <= 0x1p30f;
+    const float rs = 1.0f / s;
     if (tid == 0 && k0) f(comp_key(k0, 0));
+    uint4 cur[NL], nxt[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) cur[j] = load_group<DT, VEC>(rowp, (j * kFinThreads + tid) * EPL, V);
     for (int lo = 0; lo < V; lo += kChunk) {
         const int hi = min(lo + kChunk, V);
-        uint4 raw[NL];
-#pragma unroll
-        for (int j = 0; j < NL; ++j) raw[j] = load_group<DT, VEC>(rowp, lo + (j * kFinThreads + tid) * EPL, V);
         if (pen) recount(S, a, row, lo, hi);
+        if (hi < V) {
+#pragma unroll
+            for (int j = 0; j < NL; ++j) nxt[j] = load_group<DT, VEC>(rowp, hi + (j * kFinThreads + tid) * EPL, V);
+        }
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
             const int e0 = lo + (j * kFinThreads + tid) * EPL;
@@ -226,16 +234,21 @@ FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, 
             for (int e = 0; e < EPL; ++e) {
                 const int idx = e0 + e;
                 if (idx >= V || idx == 0) continue;
-                float x = lane_get<DT>(raw[j], e);
+                float x = lane_get<DT>(cur[j], e);
                 if (pen) {
                     const uint32_t cc = S.cnt[idx - lo];
                     if (cc) x = penalize(x, rep, pres, freq, cc);
                 }
-                const float y = s == 1.0f ? x + 0.0f : scaled(x, s);
+                float y;
+                if (s == 1.0f) y = x + 0.0f;
+                else if (mark && markstein_ok(x)) y = div_markstein(x, s, rs) + 0.0f;
+                else y = scaled(x, s);
                 f(comp_key(fkey(y), (uint32_t)idx));
             }
         }
         if (pen) __syncthreads();
+#pragma unroll
+        for (int j = 0; j < NL; ++j) cur[j] = nxt[j];
     }
     __syncthreads();
 }
@@ -492,6 +505,7 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
             atomicAdd((unsigned long long*)&S.pm_hi[b], (unsigned long long)(w >> 64));
         }
     });
+    FIE_MARK(12);
     int cur = -1, ncur = 0;   // the bin held in S.cand, its element count
     auto gather = [&](int b) -> bool {
         if (b == cur) return true;
@@ -555,7 +569,9 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
             T = above;                            // every survivor; no cut (Sv == 0)
         } else {
             if (!gather(b)) return false;
+            FIE_MARK(13);
             const SelResult r = lds_select<true>(S, ncur, Pred{tau, 0, 0}, thr - 1 - above);
+            FIE_MARK(14);
             if (!r.found) return false;
             cut = r.comp;
             T = above + r.excl + r.meas;
@@ -578,6 +594,7 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
         u128 above;
         const int b = dbin_pick<true>(S, bc, lastc, g, &above);
         if (b < 0 || !gather(b)) return false;
+        FIE_MARK(15);
         const SelResult r = lds_select<true>(S, ncur, Pred{tau, 0, cut}, g - above);
         if (!r.found) return false;
         tok = r.comp;
@@ -588,6 +605,65 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
     *T_out = T;
     *tok_out = tok;
     return true;
+}
+
+// The shortest R2 prefix of the complete candidates S.cand[0, nv) holding at least
+// `cnt` elements and, when use_mass, mass above g, moved to S.cand[0, m); returns m
+// (nv, untouched, when no shorter prefix qualifies or it would not fit the staging
+// area).  The prefix is a union of d-bins (dbin_key), located on a count and mass
+// histogram of the candidates, so the sort that follows handles only the elements a
+// top-k threshold, a top-p cut, a draw or top-L logprobs can reach.
+FIE_DEV int narrow_candidates(FinSmem& S, int nv, float M, int cnt, bool use_mass, u128 g)
+{
+    const int tid = threadIdx.x;
+    for (int i = tid; i < kPassBins; i += kFinThreads) {
+        S.pc[i] = 0;
+        S.pm_lo[i] = 0;
+        S.pm_hi[i] = 0;
+    }
+    __syncthreads();
+    for (int i = tid; i < nv; i += kFinThreads) {
+        const uint64_t c = S.cand[i];
+        const int b = dbin_key(M, comp_k(c));
+        atomicAdd(&S.pc[b], 1u);
+        if (use_mass) {
+            const u128 w = comp_weight(S, c);
+            const uint64_t lo = (uint64_t)w;
+            const uint64_t old = atomicAdd((unsigned long long*)&S.pm_lo[b], (unsigned long long)lo);
+            const uint64_t hi = (uint64_t)(w >> 64) + ((old + lo < old) ? 1ull : 0ull);
+            if (hi) atomicAdd((unsigned long long*)&S.pm_hi[b], (unsigned long long)hi);
+        }
+    }
+    __syncthreads();
+    u128 above;
+    int bs = 0;
+    if (cnt > 0) {
+        bs = dbin_pick<false>(S, kPassBins - 1, (u128)S.pc[kPassBins - 1], (u128)(cnt - 1), &above);
+        if (bs < 0) return nv;
+    }
+    if (use_mass) {
+        const int b2 = dbin_pick<true>(S, kPassBins - 1, bin_mass(S, kPassBins - 1), g, &above);
+        if (b2 < 0) return nv;
+        bs = b2 > bs ? b2 : bs;
+    }
+    constexpr int kStage = kChunk / 2;           // S.cnt holds this many composites
+    uint64_t* tmp = (uint64_t*)S.cnt;
+    if (tid == 0) S.n = 0;
+    __syncthreads();
+    for (int i = tid; i < nv; i += kFinThreads) {
+        const uint64_t c = S.cand[i];
+        if (dbin_key(M, comp_k(c)) <= bs) {
+            const uint32_t at = atomicAdd(&S.n, 1u);
+            if (at < (uint32_t)kStage) tmp[at] = c;
+        }
+    }
+    __syncthreads();
+    const int m = (int)S.n;
+    __syncthreads();
+    if (m > kStage || m >= nv) return nv;
+    for (int i = tid; i < m; i += kFinThreads) S.cand[i] = tmp[i];
+    __syncthreads();
+    return m;
 }
 
 // Token 0 keeps its penalty iff the row is the widest of the batch (no pad entry
@@ -953,6 +1029,22 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
         if (nv > kSortMax) {
             deep = true;
         } else {
+            // what the selections below can reach: top-k and top-L by count; a
+            // top-p cut (over the whole row: no top-k, no min-p) or a plain draw by
+            // mass; min-p rows sort every candidate
+            const int L = lp > 0 ? (lp < a.lp_cols ? lp : a.lp_cols) : 0;
+            int cnt = L;
+            bool by_mass = false;
+            u128 g = 0;
+            bool narrow = nv > 384;
+            if (!greedy) {
+                if (mp > 0.0f) narrow = false;
+                else if (topk > 0) cnt = topk > cnt ? topk : cnt;
+                else if (tp < 1.0f) { by_mass = true; g = ceil_mul_f32(tp, sall) - 1; }
+                else { by_mass = true; g = floor_mul_f64(a.uniform[row], sall); }
+                if (by_mass && sall == 0) narrow = false;
+            }
+            if (narrow && (cnt > 0 || by_mass)) nv = narrow_candidates(S, nv, M, cnt, by_mass, g);
             sort_desc(S, nv);
             sorted = true;
         }

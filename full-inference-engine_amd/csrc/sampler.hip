@@ -241,10 +241,6 @@ static bool vec_ok(const void* p, int64_t stride, int sz)
 template <int DT>
 static int launch_scan(const KParams& P, bool vec, bool longh, hipStream_t st)
 {
-    if (P.a.apply_penalties) {
-        k_prep<<<P.a.rows, kPrepThreads, 0, st>>>(P);
-        FIE_LAUNCH_CHECK("k_prep");
-    }
     const dim3 grid(P.NS, P.a.rows);
     if (vec) {
         if (longh) k_scan<DT, true, true><<<grid, kScanThreads, 0, st>>>(P);
@@ -271,6 +267,13 @@ static int run_stage(const KParams& P, int stage, hipStream_t st)
     const int sz = P.a.dtype == FIE_F32 ? 4 : 2;
     const bool vec = vec_ok(P.a.logits, P.a.row_stride, sz);
     const bool longh = P.a.apply_penalties && P.a.max_row_hist > 65535;
+    if (stage == FIE_STAGE_PREP) {
+        if (P.a.apply_penalties) {
+            k_prep<<<P.a.rows, kPrepThreads, 0, st>>>(P);
+            FIE_LAUNCH_CHECK("k_prep");
+        }
+        return FIE_OK;
+    }
     if (stage == FIE_STAGE_SCAN) {
         switch (P.a.dtype) {
         case FIE_F32: return launch_scan<FIE_F32>(P, vec, longh, st);
@@ -342,6 +345,8 @@ int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, vo
     int rc = prepare(args, ws, &P);
     if (rc != FIE_OK || args->rows == 0) return rc;
     hipStream_t st = (hipStream_t)stream;
+    rc = run_stage(P, FIE_STAGE_PREP, st);
+    if (rc != FIE_OK) return rc;
     rc = run_stage(P, FIE_STAGE_SCAN, st);
     if (rc != FIE_OK) return rc;
     return run_stage(P, FIE_STAGE_FINISH, st);
@@ -349,7 +354,8 @@ int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, vo
 
 int fie_sampler_stage(const fie_sampler_args* args, const fie_workspace* ws, int32_t stage, void* stream)
 {
-    if (stage != FIE_STAGE_SCAN && stage != FIE_STAGE_FINISH) return fail(FIE_E_ARG, "unknown stage");
+    if (stage != FIE_STAGE_PREP && stage != FIE_STAGE_SCAN && stage != FIE_STAGE_FINISH)
+        return fail(FIE_E_ARG, "unknown stage");
     KParams P;
     int rc = prepare(args, ws, &P);
     if (rc != FIE_OK || args->rows == 0) return rc;

@@ -203,16 +203,26 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep(const KParams P)
     __syncthreads();
     const int64_t h0 = a.hist_offsets[row], h1 = a.hist_offsets[row + 1];
     uint16_t* bk = P.w.bk + (size_t)row * NS * kBucketCap;
-    for (int64_t h = h0 + tid; h < h1; h += kPrepThreads) {
-        const uint32_t id = (uint32_t)a.hist_ids[h];
-        if (id == 0) {
-            atomicAdd(&zc, 1u);
-        } else if (id < V) {
-            const uint32_t sp = id / (uint32_t)kSpan;
-            const uint32_t at = atomicAdd(&sc[sp], 1u);
-            if (at < (uint32_t)kBucketCap) bk[sp * kBucketCap + at] = (uint16_t)(id % (uint32_t)kSpan);
-        } else {
-            atomicAdd(&badc, 1u);
+    constexpr int kPer = 8;   // ids per thread per batch, loaded together
+    for (int64_t base = h0; base < h1; base += (int64_t)kPer * kPrepThreads) {
+        uint32_t ids[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int64_t h = base + q * kPrepThreads + tid;
+            ids[q] = h < h1 ? (uint32_t)a.hist_ids[h] : 0xFFFFFFFFu;
+        }
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const uint32_t id = ids[q];
+            if (id == 0) {
+                atomicAdd(&zc, 1u);
+            } else if (id < V) {
+                const uint32_t sp = id / (uint32_t)kSpan;
+                const uint32_t at = atomicAdd(&sc[sp], 1u);
+                if (at < (uint32_t)kBucketCap) bk[sp * kBucketCap + at] = (uint16_t)(id % (uint32_t)kSpan);
+            } else if (base + q * kPrepThreads + tid < h1) {
+                atomicAdd(&badc, 1u);
+            }
         }
     }
     __syncthreads();

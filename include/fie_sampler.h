@@ -129,8 +129,9 @@ int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, vo
    workspace each time).  No counterpart in the reference: it exists so a profiler
    or a benchmark can time each kernel of the chain separately. */
 enum {
-    FIE_STAGE_SCAN = 0,        /* the streaming pass over the logits */
-    FIE_STAGE_FINISH = 1,      /* the per-row selection and draw */
+    FIE_STAGE_PREP = 0,        /* the penalty histories bucketed by span (no-op without penalties) */
+    FIE_STAGE_SCAN = 1,        /* the streaming pass over the logits */
+    FIE_STAGE_FINISH = 2,      /* the per-row selection and draw */
 };
 int fie_sampler_stage(const fie_sampler_args* args, const fie_workspace* ws, int32_t stage,
                       void* stream);
