@@ -122,6 +122,33 @@ FIE_DEV bool markstein_ok(float x)
     return a >= 0x1p-96f && a <= 0x1p96f;
 }
 
+// ---------------------------------------------------------------- counter-based draws
+// Philox4x64-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as
+// 1, 2, 3", SC 2011): ten rounds of two 64x64->128 multiplies by the published
+// multipliers, the key bumped by the published Weyl constants between rounds.
+FIE_DEV void philox4x64_10(uint64_t (&x)[4], uint64_t k0, uint64_t k1)
+{
+    constexpr uint64_t kM0 = 0xD2E7470EE14C6C93ull, kM1 = 0xCA5A826395121157ull;
+    constexpr uint64_t kW0 = 0x9E3779B97F4A7C15ull, kW1 = 0xBB67AE8584CAA73Bull;
+#pragma unroll
+    for (int r = 0; r < 10; ++r) {
+        if (r) { k0 += kW0; k1 += kW1; }
+        const uint64_t lo0 = kM0 * x[0], hi0 = __umul64hi(kM0, x[0]);
+        const uint64_t lo1 = kM1 * x[2], hi1 = __umul64hi(kM1, x[2]);
+        const uint64_t y0 = hi1 ^ x[1] ^ k0, y2 = hi0 ^ x[3] ^ k1;
+        x[0] = y0; x[1] = lo1; x[2] = y2; x[3] = lo0;
+    }
+}
+
+// The draw of one (key0, key1, counter) triple: the block's first word as a double
+// in [0, 1) with 53 random bits.
+FIE_DEV double philox_uniform(const uint64_t* t)
+{
+    uint64_t x[4] = {t[2], 0, 0, 0};
+    philox4x64_10(x, t[0], t[1]);
+    return (double)(x[0] >> 11) * 0x1p-53;
+}
+
 // floor(e * 2^40) of e in [0, 1].  e * 2^40 is exact in double, so the conversion
 // only truncates.
 FIE_DEV uint64_t fixed40(float e)

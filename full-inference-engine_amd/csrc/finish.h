@@ -931,6 +931,8 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
     const bool need_mass = lp >= 0 || (!greedy && topk == 0);
     float rep = 1.0f, pres = 0.0f, freq = 0.0f;
     if (pen) { rep = a.repetition[row]; pres = a.presence[row]; freq = a.frequency[row]; }
+    // the row's draw: on-device counter-based, or the caller's
+    const double urow = greedy ? 0.0 : (a.rng ? philox_uniform(a.rng + 3 * (size_t)row) : a.uniform[row]);
     int32_t status = 0;
     if (pen && P.w.bad[row] && !a.hist_invalid) status |= FIE_ROW_UNCOUNTED_IDS;
 
@@ -1041,7 +1043,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
                 if (mp > 0.0f) narrow = false;
                 else if (topk > 0) cnt = topk > cnt ? topk : cnt;
                 else if (tp < 1.0f) { by_mass = true; g = ceil_mul_f32(tp, sall) - 1; }
-                else { by_mass = true; g = floor_mul_f64(a.uniform[row], sall); }
+                else { by_mass = true; g = floor_mul_f64(urow, sall); }
                 if (by_mass && sall == 0) narrow = false;
             }
             if (narrow && (cnt > 0 || by_mass)) nv = narrow_candidates(S, nv, M, cnt, by_mass, g);
@@ -1086,7 +1088,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
                     token = comp_idx(cmax);
                     tok_comp = cmax;
                 } else {
-                    const u128 g = floor_mul_f64(a.uniform[row], T);
+                    const u128 g = floor_mul_f64(urow, T);
                     u128 incl;
                     const int i = chunk_find(S, ch, g, lim, &incl);
                     if (i < 0) deep = true;
@@ -1105,7 +1107,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
         cut = 0;
         uint32_t tk = 0;
         const bool binned = binned_deep<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, M, topk, mp, tp,
-                                                 a.uniform[row], sall, &tk, &tau, &cut, &T, &tok_comp);
+                                                 urow, sall, &tk, &tau, &cut, &T, &tok_comp);
         if (!binned) {
         // radix levels over the composite, re-reading the row per level
         cut = 0;
@@ -1139,7 +1141,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
                                                            Pred{0, 0, 0}, 0, false);
             tok_comp = r.comp;
         } else {
-            const u128 g = floor_mul_f64(a.uniform[row], T);
+            const u128 g = floor_mul_f64(urow, T);
             const SelResult r = row_select<DT, VEC, true>(S, P, row, s, pen, rep, pres, freq, k0,
                                                           Pred{tau, 0, cut}, g, l1);
             tok_comp = r.comp;

@@ -1,10 +1,12 @@
 // MI355X fused token sampler: kernels behind the C ABI of include/fie_sampler.h.
 //
+//   k_prep      penalty histories bucketed by span                (scan.h)
 //   k_scan      one streaming read of the logits, tile partials   (scan.h)
 //   k_finish    one workgroup per row: exact selection and draw   (finish.h)
 //   k_argmax_*  the greedy fast path, logits.argmax(-1)           (sampler.py:106)
 //   k_kept      kept set / probabilities of the last step (verification aid)
 //   k_cexp      the canonical exponential (verification aid)
+//   k_uniforms  the on-device counter-based draws (verification aid)
 #include <hip/hip_runtime.h>
 
 #include <stdio.h>
@@ -130,6 +132,12 @@ __global__ __launch_bounds__(kScanThreads) void k_kept(const KParams P, uint8_t*
     }
 }
 
+__global__ void k_uniforms(const uint64_t* rng, double* out, int32_t rows)
+{
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r < rows) out[r] = philox_uniform(rng + 3 * (size_t)r);
+}
+
 __global__ void k_cexp(const float* in, float* out, int64_t n)
 {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -215,7 +223,8 @@ static int check_args(const fie_sampler_args* a)
     if (a->lp_cols < 0 || a->lp_cols > 20) return fail(FIE_E_ARG, "lp_cols out of range [0, 20]");
     if (a->row_stride < a->vocab) return fail(FIE_E_ARG, "row_stride < vocab");
     if (a->rows == 0) return FIE_OK;
-    if (!a->logits || !a->tokens || !a->scale || !a->top_k || !a->top_p || !a->min_p || !a->flags || !a->uniform)
+    if (!a->logits || !a->tokens || !a->scale || !a->top_k || !a->top_p || !a->min_p || !a->flags ||
+        (!a->uniform && !a->rng))
         return fail(FIE_E_ARG, "a required pointer is NULL");
     if (a->apply_penalties && (!a->repetition || !a->presence || !a->frequency || !a->hist_offsets || !a->hist_ids))
         return fail(FIE_E_ARG, "penalties applied but a penalty pointer is NULL");
@@ -422,6 +431,15 @@ int fie_sampler_cexp(const float* in, float* out, int64_t n, void* stream)
     if (n == 0) return FIE_OK;
     k_cexp<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(in, out, n);
     FIE_LAUNCH_CHECK("k_cexp");
+    return FIE_OK;
+}
+
+int fie_sampler_uniforms(const uint64_t* rng, double* out, int32_t rows, void* stream)
+{
+    if (rows < 0 || (rows > 0 && (!rng || !out))) return fail(FIE_E_ARG, "bad uniforms arguments");
+    if (rows == 0) return FIE_OK;
+    k_uniforms<<<(rows + 255) / 256, 256, 0, (hipStream_t)stream>>>(rng, out, rows);
+    FIE_LAUNCH_CHECK("k_uniforms");
     return FIE_OK;
 }
 

@@ -5,12 +5,16 @@ of the reference (engine/batching/sampler.py:32-117), so the engine's ``_sample`
 adapter (engine/batching/continuous_batching.py:1911-1931) can call it unchanged.
 What changes is underneath: one packed parameter upload, a fixed chain of fused HIP
 kernels, one packed download.  The draw is an inverse-CDF draw against a per-row
-uniform taken from the row's own generator (seeded rows) or the shared generator,
-so a seeded request's tokens do not depend on its batch neighbours.
+uniform that the kernel derives on the device from a counter-based generator
+(Philox4x64-10): a seeded request draws from its own stream, keyed by its seed and
+advanced per request, so its tokens do not depend on its batch neighbours; the
+other rows share one stream keyed by ``generator_seed``.  The host keeps only
+counters.
 """
 
 from __future__ import annotations
 
+import os
 from collections import OrderedDict
 from dataclasses import dataclass
 
@@ -67,10 +71,14 @@ def pack_history(contexts: list[list[int]], include: np.ndarray, vocab: int):
 _EMPTY = np.zeros(0, dtype=np.int64)
 
 
-def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarray,
-                   contexts: list[list[int]] | None) -> HostParams:
-    """Per-row arrays for the kernels, derived the way sampler.py:109,182-192 does."""
+def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarray | None,
+                   contexts: list[list[int]] | None, rng: np.ndarray | None = None) -> HostParams:
+    """Per-row arrays for the kernels, derived the way sampler.py:109,182-192 does.
+    The draws are `uniforms` (float64 [rows]) or, when `rng` (uint64 [rows, 3]) is
+    given, derived on the device from it."""
     rows = len(params)
+    if uniforms is None:
+        uniforms = np.zeros(rows, dtype=np.float64)
     greedy = np.fromiter((p.greedy for p in params), dtype=bool, count=rows)
     pen = np.fromiter((p.has_penalties for p in params), dtype=bool, count=rows)
     temps = np.fromiter((p.temperature for p in params), dtype=np.float64, count=rows)
@@ -100,15 +108,22 @@ def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarra
         apply_penalties=apply,
         hist_invalid=invalid,
         max_row_hist=longest,
+        rng=None if rng is None else np.ascontiguousarray(rng, dtype=np.uint64).reshape(rows, 3),
     )
+
+
+# Second key words of the two kinds of draw streams: a seeded request's stream is
+# keyed (seed, SEEDED), the shared stream (generator_seed, SHARED).
+SEEDED_STREAM = 0x5EEDED5EEDED5EED
+SHARED_STREAM = 0x5A4ED5A4ED5A4ED5
 
 
 class BatchedSampler:
     """Applies per-request sampling to one step's logits (sampler.py:42-78).
 
-    Holds no per-request state besides the seeded generators: penalties come from
-    the token ids the caller passes, so a preempted and rebuilt request samples
-    identically.
+    Holds no per-request state besides the draw counters of seeded requests:
+    penalties come from the token ids the caller passes, so a preempted and rebuilt
+    request samples identically.
     """
 
     def __init__(self, device: torch.device | str, *, generator_seed: int | None = None,
@@ -116,41 +131,44 @@ class BatchedSampler:
         self.device = torch.device(device)
         self._fused = FusedSampler(self.device)
         # The shared stream for rows without their own seed.
-        self._generator = np.random.Generator(np.random.PCG64(generator_seed))
-        # Request id -> generator (sampler.py:58-61): two requests with one seed must
-        # not share a stream, so generators are keyed by request, not by seed.
-        self._seeded: OrderedDict[object, np.random.Generator] = OrderedDict()
+        self._shared_key = (int(generator_seed) if generator_seed is not None
+                            else int.from_bytes(os.urandom(8), "little")) & 0xFFFFFFFFFFFFFFFF
+        self._shared_draws = 0
+        # Request id -> draws taken so far (sampler.py:58-61): two requests with one
+        # seed must not share a stream position, so counters are kept per request,
+        # not per seed; at most max_generators of them, least recently used dropped.
+        self._seeded: OrderedDict[object, int] = OrderedDict()
         self._max_generators = max_generators
 
-    def _row_generator(self, request_id: object, seed: int) -> np.random.Generator:
-        gen = self._seeded.get(request_id)
-        if gen is None:
-            gen = np.random.Generator(np.random.PCG64(seed))
-            self._seeded[request_id] = gen
-            while len(self._seeded) > self._max_generators:
-                self._seeded.popitem(last=False)
-        else:
-            self._seeded.move_to_end(request_id)
-        return gen
+    def _next_draw(self, request_id: object) -> int:
+        n = self._seeded.pop(request_id, 0) + 1
+        self._seeded[request_id] = n
+        while len(self._seeded) > self._max_generators:
+            self._seeded.popitem(last=False)
+        return n
 
     def forget(self, request_ids: list[object]) -> None:
-        """Drop generators for finished requests (sampler.py:75-78)."""
+        """Drop the streams of finished requests (sampler.py:75-78)."""
         for request_id in request_ids:
             self._seeded.pop(request_id, None)
 
-    def _uniforms(self, params: list[SamplingParams],
-                  request_ids: list[object] | None) -> np.ndarray:
+    def _draw_keys(self, params: list[SamplingParams],
+                   request_ids: list[object] | None) -> np.ndarray:
+        """uint64 [rows, 3] (key0, key1, counter) per row: a seeded row's request
+        stream at its next position, the shared stream in row order otherwise
+        (greedy rows draw nothing)."""
         rows = len(params)
-        u = np.zeros(rows, dtype=np.float64)
-        unseeded = [r for r, p in enumerate(params) if not p.greedy and p.seed is None]
-        if unseeded:
-            u[unseeded] = self._generator.random(len(unseeded))
+        keys = np.zeros((rows, 3), dtype=np.uint64)
         for r, p in enumerate(params):
-            if p.greedy or p.seed is None:
+            if p.greedy:
                 continue
-            rid = request_ids[r] if request_ids is not None else r
-            u[r] = self._row_generator(rid, p.seed).random()
-        return u
+            if p.seed is None:
+                self._shared_draws += 1
+                keys[r] = (self._shared_key, SHARED_STREAM, self._shared_draws)
+            else:
+                rid = request_ids[r] if request_ids is not None else r
+                keys[r] = (p.seed, SEEDED_STREAM, self._next_draw(rid))
+        return keys
 
     # ------------------------------------------------------------------ the step
     def sample(
@@ -179,7 +197,8 @@ class BatchedSampler:
             # sampler.py:103-106: one argmax kernel and one device-to-host copy.
             return SampleResult(self._fused.argmax(logits).tolist(), {})
 
-        hp = resolve_params(params, vocab, self._uniforms(params, request_ids), context_tokens)
+        hp = resolve_params(params, vocab, None, context_tokens,
+                            rng=self._draw_keys(params, request_ids))
         out, _, _ = self._fused.step(logits, hp)
         tokens = [int(t) for t in out["tokens"]]
         return SampleResult(tokens, self._logprobs(params, tokens, out))

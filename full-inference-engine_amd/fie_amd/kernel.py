@@ -19,12 +19,13 @@ from ._lib import LP_COLS, SamplerArgs, Workspace
 _DTYPES = {torch.float32: _lib.FIE_F32, torch.float16: _lib.FIE_F16,
            torch.bfloat16: _lib.FIE_BF16}
 
-# Per-row parameter arrays in upload order.
+# Per-row parameter arrays in upload order: (name, dtype, values per row).
 PARAM_FIELDS = (
-    ("scale", np.float32), ("top_k", np.int32), ("top_p", np.float32), ("min_p", np.float32),
-    ("flags", np.int32), ("logprobs", np.int32), ("uniform", np.float64),
-    ("rep", np.float32), ("pres", np.float32), ("freq", np.float32),
-    ("hist_invalid", np.int32),
+    ("scale", np.float32, 1), ("top_k", np.int32, 1), ("top_p", np.float32, 1),
+    ("min_p", np.float32, 1), ("flags", np.int32, 1), ("logprobs", np.int32, 1),
+    ("uniform", np.float64, 1), ("rng", np.uint64, 3),
+    ("rep", np.float32, 1), ("pres", np.float32, 1), ("freq", np.float32, 1),
+    ("hist_invalid", np.int32, 1),
 )
 # Per-row outputs in download order: (name, dtype, values per row).
 OUTPUT_FIELDS = (
@@ -66,6 +67,7 @@ class HostParams:
     apply_penalties: bool
     hist_invalid: np.ndarray | None = None   # int32 [rows], rows with ids >= vocab
     max_row_hist: int = 0
+    rng: np.ndarray | None = None            # uint64 [rows, 3]: on-device draws (key0, key1, counter)
 
     @property
     def rows(self) -> int:
@@ -80,9 +82,9 @@ class DeviceStep:
         self.rows = rows
         self.hist_cap = hist_cap
         offs, o = {}, 0
-        for name, dt in PARAM_FIELDS:
+        for name, dt, width in PARAM_FIELDS:
             offs[name] = o
-            o = _align(o + max(rows, 1) * np.dtype(dt).itemsize)
+            o = _align(o + max(rows, 1) * width * np.dtype(dt).itemsize)
         offs["hist_off"] = o
         o = _align(o + (rows + 1) * 8)
         offs["hist_ids"] = o
@@ -107,10 +109,10 @@ class DeviceStep:
         return self.base + self.offs[name]
 
     def stage(self, hp: HostParams) -> None:
-        for name, dt in PARAM_FIELDS:
+        for name, dt, width in PARAM_FIELDS:
             src = getattr(hp, name)
             if src is not None:
-                self.host_view(name, dt, self.rows)[:] = src
+                self.host_view(name, dt, self.rows * width)[:] = np.asarray(src).reshape(-1)
         self.host_view("hist_off", np.int64, self.rows + 1)[:] = hp.hist_off
         n = int(hp.hist_off[-1])
         if n:
@@ -207,6 +209,7 @@ class FusedSampler:
         a.kept_mass, a.row_mass = buf.ptr("kept_mass"), buf.ptr("row_mass")
         a.chosen_logprob = buf.ptr("chosen_lp")
         a.top_ids, a.top_logprobs = buf.ptr("top_ids"), buf.ptr("top_lp")
+        a.rng = buf.ptr("rng") if hp.rng is not None else None
         a._keep = logits  # the converted tensor must outlive the launch
         return a
 
@@ -250,6 +253,15 @@ class FusedSampler:
         out = torch.empty_like(values)
         _lib.check(self.lib.fie_sampler_cexp(values.data_ptr(), out.data_ptr(), values.numel(),
                                              self._stream_ptr()), "fie_sampler_cexp")
+        return out
+
+    def uniforms(self, rng: torch.Tensor) -> torch.Tensor:
+        """The on-device draws of uint64 (key0, key1, counter) triples [rows, 3]
+        (verification of what the sampler derives when ``HostParams.rng`` is set)."""
+        rows = rng.shape[0]
+        out = torch.empty(rows, dtype=torch.float64, device=self.device)
+        _lib.check(self.lib.fie_sampler_uniforms(rng.data_ptr(), out.data_ptr(), rows,
+                                                 self._stream_ptr()), "fie_sampler_uniforms")
         return out
 
     # ------------------------------------------------------------------ a full step

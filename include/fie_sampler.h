@@ -75,7 +75,8 @@ typedef struct fie_sampler_args {
     const int32_t* flags;       /* FIE_FLAG_* bits */
     const int32_t* logprobs;    /* -1 = no logprobs, else the row's count 0..20; may be
                                    NULL when no row asks for logprobs */
-    const double* uniform;      /* caller-supplied draw in [0,1) per row */
+    const double* uniform;      /* caller-supplied draw in [0,1) per row; may be NULL
+                                   when `rng` is given */
 
     /* Penalties (sampler.py:109-110,120-175).  apply_penalties is the batch gate
        "some row has penalties and contexts were passed"; the history is CSR and
@@ -105,6 +106,14 @@ typedef struct fie_sampler_args {
     float* chosen_logprob;      /* [rows] (rows with logprobs >= 0) */
     int64_t* top_ids;           /* [rows, lp_cols] (-1 past the row's count) */
     float* top_logprobs;        /* [rows, lp_cols] */
+
+    /* On-device draws (optional; replaces the per-request generators of
+       sampler.py:58-73).  When non-NULL, row r's uniform is derived on the device
+       from rng[3r .. 3r+2] = (key0, key1, counter): the first 64-bit word x of the
+       Philox4x64-10 block (Salmon et al., SC 2011) at counter (counter, 0, 0, 0) and
+       key (key0, key1), as (x >> 11) * 2^-53, and `uniform` is not read.  The
+       caller keeps one key per stream and advances its counter per draw. */
+    const uint64_t* rng;
 } fie_sampler_args;
 
 /* Device workspace owned by the caller: `bytes` of device memory at `ptr`
@@ -151,6 +160,10 @@ int fie_sampler_kept(const fie_sampler_args* args, uint8_t* kept, float* probs,
 
 /* The build's canonical fp32 exponential on n device values (verification aid). */
 int fie_sampler_cexp(const float* in, float* out, int64_t n, void* stream);
+
+/* The on-device uniforms of `rng` (see fie_sampler_args) for `rows` rows into
+   out[rows] (verification; no counterpart in the reference). */
+int fie_sampler_uniforms(const uint64_t* rng, double* out, int32_t rows, void* stream);
 
 /* Message of the last failing call on this thread (static storage). */
 const char* fie_sampler_last_error(void);

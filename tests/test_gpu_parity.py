@@ -297,6 +297,50 @@ def test_seeded_rows_are_batch_independent(fs):
     assert alone == with_others
 
 
+def _philox_uniform(key0, key1, counter):
+    """numpy's Philox4x64-10 generator at the kernel's block (numpy advances its
+    counter before a block, hence counter - 1)."""
+    g = np.random.Generator(np.random.Philox(key=int(key0) | (int(key1) << 64), counter=int(counter) - 1))
+    return g.random()
+
+
+def test_device_uniforms_match_numpys_philox(fs):
+    rng = np.random.default_rng(17)
+    keys = rng.integers(0, 2**63, size=(300, 3), dtype=np.uint64)
+    keys[:, 2] = rng.integers(1, 2**40, size=300, dtype=np.uint64)
+    keys[0] = (0, 0, 1)
+    keys[1] = (2**64 - 1, 2**64 - 1, 2**64 - 1)
+    got = fs.uniforms(torch.from_numpy(keys.view(np.int64)).to(DEV)).cpu().numpy()
+    want = np.array([_philox_uniform(*k) for k in keys])
+    np.testing.assert_array_equal(got, want)
+
+
+def test_batched_sampler_draws_on_device_like_the_oracle(fs):
+    """BatchedSampler's rows draw on the device from (seed or shared key, stream,
+    counter); the oracle, given the same uniforms from numpy's Philox, picks the
+    same tokens, over two steps (the counters advance)."""
+    from fie_amd.batching.sampler import SEEDED_STREAM, SHARED_STREAM
+    rng = np.random.default_rng(23)
+    rows, vocab = 12, 30000
+    x = torch.from_numpy(rng.normal(0, 1.5, (rows, vocab)).astype(np.float32)).to(DEV)
+    params = [SamplingParams(temperature=1.0, top_p=0.95, seed=(77 if r % 3 == 0 else None))
+              for r in range(rows)]
+    ids = [f"q{r}" for r in range(rows)]
+    s = BatchedSampler(DEV, generator_seed=4242)
+    shared = 0
+    for step in (1, 2):
+        res = s.sample(x, params, None, ids)
+        u = []
+        for r, p in enumerate(params):
+            if p.seed is None:
+                shared += 1
+                u.append(_philox_uniform(4242, SHARED_STREAM, shared))
+            else:
+                u.append(_philox_uniform(p.seed, SEEDED_STREAM, step))
+        ref = O.canonical_step(x.cpu().numpy(), O.resolve(params, vocab), np.array(u))
+        assert res.token_ids == ref.tokens.tolist(), step
+
+
 def test_c_abi_direct_calls_and_errors(fs):
     lib = _lib.load()
     ws = fs.ensure_workspace(4, 1000)

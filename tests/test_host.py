@@ -14,7 +14,8 @@ import numpy as np
 import pytest
 
 from fie_amd import _lib
-from fie_amd.batching.sampler import BatchedSampler, SampleResult, pack_history, resolve_params
+from fie_amd.batching.sampler import (SEEDED_STREAM, SHARED_STREAM, BatchedSampler, SampleResult,
+                                      pack_history, resolve_params)
 from fie_amd.kernel import FLAG_GREEDY, FLAG_PENALTY
 from fie_amd.runtime.sampling import GREEDY, SamplingParams
 
@@ -128,11 +129,12 @@ def test_resolve_params_follows_the_reference_row_rules():
 # ---------------------------------------------------------------- the adapter's calls
 class _NoKernels(BatchedSampler):
     """BatchedSampler with its host state only (the constructor's device setup is
-    skipped): exercises validation, uniforms and logprob assembly on the CPU."""
+    skipped): exercises validation, draw keys and logprob assembly on the CPU."""
 
     def __init__(self, generator_seed=None, max_generators=1024):
         from collections import OrderedDict
-        self._generator = np.random.Generator(np.random.PCG64(generator_seed))
+        self._shared_key = generator_seed if generator_seed is not None else 12345
+        self._shared_draws = 0
         self._seeded = OrderedDict()
         self._max_generators = max_generators
 
@@ -153,29 +155,60 @@ def test_sample_validation_errors():
     assert s.sample(torch.zeros(0, 5), []) == SampleResult([], {})
 
 
-def test_seeded_rows_are_reproducible_per_request():
-    """sampler.py:58-73: a seeded request draws from its own generator, keyed by
-    request id (two requests with one seed do not share a stream), unaffected by
-    the rest of the batch; forget() starts it over."""
+def test_seeded_rows_draw_from_their_own_request_stream():
+    """sampler.py:58-73: a seeded request draws from its own stream (keyed by its
+    seed, positioned per request id: two requests with one seed do not share a
+    position), unaffected by the rest of the batch; forget() starts it over."""
     p = SamplingParams(temperature=1.0, seed=7)
     q = SamplingParams(temperature=1.0)
     a = _NoKernels(generator_seed=1)
-    u1 = a._uniforms([p, q, p], ["r1", "x", "r2"])
-    assert u1[0] == u1[2]                       # same seed, different requests
+    k1 = a._draw_keys([p, q, p], ["r1", "x", "r2"])
+    assert k1[0].tolist() == [7, SEEDED_STREAM, 1] and k1[2].tolist() == [7, SEEDED_STREAM, 1]
+    assert k1[1].tolist() == [1, SHARED_STREAM, 1]
     b = _NoKernels(generator_seed=99)
-    u2 = b._uniforms([q, q, p], ["y", "z", "r1"])
-    assert u2[2] == u1[0]                       # batch-independent
-    assert a._uniforms([p], ["r1"])[0] != u1[0]  # the stream advances
+    k2 = b._draw_keys([q, q, p], ["y", "z", "r1"])
+    assert k2[2].tolist() == k1[0].tolist()         # batch-independent
+    assert a._draw_keys([p], ["r1"])[0, 2] == 2      # the stream advances
     a.forget(["r1"])
-    assert a._uniforms([p], ["r1"])[0] == u1[0]  # and restarts after forget
-    assert a._uniforms([GREEDY], ["g"])[0] == 0.0
+    assert a._draw_keys([p], ["r1"])[0, 2] == 1      # and restarts after forget
+    assert a._draw_keys([GREEDY], ["g"]).tolist() == [[0, 0, 0]]
+    assert a._draw_keys([q, q], None)[:, 2].tolist() == [2, 3]   # the shared stream moves on
 
 
-def test_generator_cache_is_capped():
+def test_request_counters_are_capped():
     s = _NoKernels(max_generators=3)
     p = SamplingParams(temperature=1.0, seed=1)
-    s._uniforms([p] * 5, [f"r{i}" for i in range(5)])
+    s._draw_keys([p] * 5, [f"r{i}" for i in range(5)])
     assert list(s._seeded) == ["r2", "r3", "r4"]
+
+
+def philox_uniform_reference(key0, key1, counter):
+    """The draw the kernels derive from (key0, key1, counter), by numpy's own
+    Philox4x64-10 (an independent implementation of Salmon et al. 2011): numpy
+    advances its counter before a block, so counter - 1 starts at our block."""
+    g = np.random.Generator(np.random.Philox(key=int(key0) | (int(key1) << 64), counter=int(counter) - 1))
+    return g.random()
+
+
+def test_draw_formula_is_numpys_philox_generator():
+    """The host-side statement of the device draw (first word of the block, 53
+    bits) equals numpy's Generator(Philox).random() at that position; the GPU
+    test checks the kernel against the same function."""
+    M = (1 << 64) - 1
+    M0, M1 = 0xD2E7470EE14C6C93, 0xCA5A826395121157
+    W0, W1 = 0x9E3779B97F4A7C15, 0xBB67AE8584CAA73B
+
+    def block(ctr, k0, k1):
+        x = [ctr, 0, 0, 0]
+        for r in range(10):
+            if r:
+                k0, k1 = (k0 + W0) & M, (k1 + W1) & M
+            p0, p1 = M0 * x[0], M1 * x[2]
+            x = [(p1 >> 64) ^ x[1] ^ k0, p1 & M, (p0 >> 64) ^ x[3] ^ k1, p0 & M]
+        return x
+
+    for k0, k1, c in [(0, 0, 1), (7, SEEDED_STREAM, 3), (M, SHARED_STREAM, 123456789)]:
+        assert (block(c, k0, k1)[0] >> 11) * 2.0 ** -53 == philox_uniform_reference(k0, k1, c)
 
 
 def test_logprob_entries_follow_the_reference_layout():
