@@ -140,8 +140,9 @@ def time_config(config: int, steps: int, warmup: int, ring_mb: int, dev):
 
 
 def end_to_end_ms(w, dev, reps: int = 20) -> float:
-    """BatchedSampler.sample() as the engine calls it: parameter packing, history
-    packing, upload, the kernels, download and the host lists, per call."""
+    """BatchedSampler.sample() as the engine calls it, per decode step: parameter
+    resolution, the appended context token per row (the contexts stay on the
+    device between steps), upload, the kernels, download and the host lists."""
     import torch
 
     from fie_amd.batching.sampler import BatchedSampler
@@ -149,12 +150,16 @@ def end_to_end_ms(w, dev, reps: int = 20) -> float:
     s = BatchedSampler(dev, generator_seed=0)
     x = w.logits
     ids = [f"r{i}" for i in range(x.shape[0])]
-    s.sample(x, w.params, w.contexts, ids)
+    ctx = [list(c) for c in w.contexts] if w.contexts is not None else None
+    res = s.sample(x, w.params, ctx, ids)
     torch.cuda.synchronize()
     times = []
     for _ in range(reps):
+        if ctx is not None:
+            for c, t in zip(ctx, res.token_ids):
+                c.append(t)
         t = time.perf_counter()
-        s.sample(x, w.params, w.contexts, ids)
+        res = s.sample(x, w.params, ctx, ids)
         times.append(time.perf_counter() - t)
     return statistics.median(times) * 1e3
 

@@ -191,7 +191,7 @@ FIE_DEV void recount(FinSmem& S, const fie_sampler_args& a, int row, int lo, int
 {
     for (int i = threadIdx.x; i < kChunk; i += kFinThreads) S.cnt[i] = 0;
     __syncthreads();
-    const int64_t h0 = a.hist_offsets[row], h1 = a.hist_offsets[row + 1];
+    const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
     for (int64_t h = h0 + threadIdx.x; h < h1; h += kFinThreads) {
         const uint32_t id = (uint32_t)a.hist_ids[h];
         if (id >= (uint32_t)lo && id < (uint32_t)hi && id != 0) {

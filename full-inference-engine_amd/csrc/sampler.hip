@@ -7,6 +7,7 @@
 //   k_kept      kept set / probabilities of the last step (verification aid)
 //   k_cexp      the canonical exponential (verification aid)
 //   k_uniforms  the on-device counter-based draws (verification aid)
+//   k_history_write  appends tokens to a device-resident penalty history
 #include <hip/hip_runtime.h>
 
 #include <stdio.h>
@@ -87,7 +88,7 @@ __global__ __launch_bounds__(kScanThreads) void k_kept(const KParams P, uint8_t*
         freq = a.frequency[row];
         for (int i = tid; i < kArgChunk; i += kScanThreads) cnt[i] = 0;
         __syncthreads();
-        const int64_t h0 = a.hist_offsets[row], h1 = a.hist_offsets[row + 1];
+        const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
         for (int64_t h = h0 + tid; h < h1; h += kScanThreads) {
             const uint32_t id = (uint32_t)a.hist_ids[h];
             if (id >= (uint32_t)lo && id < (uint32_t)hi && id != 0) atomicAdd(&cnt[id - lo], 1u);
@@ -130,6 +131,12 @@ __global__ __launch_bounds__(kScanThreads) void k_kept(const KParams P, uint8_t*
             if (probs) probs[o] = p;
         }
     }
+}
+
+__global__ void k_history_write(int32_t* ids, const int64_t* dst, const int32_t* src, int64_t n)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) ids[dst[i]] = src[i];
 }
 
 __global__ void k_uniforms(const uint64_t* rng, double* out, int32_t rows)
@@ -431,6 +438,16 @@ int fie_sampler_cexp(const float* in, float* out, int64_t n, void* stream)
     if (n == 0) return FIE_OK;
     k_cexp<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(in, out, n);
     FIE_LAUNCH_CHECK("k_cexp");
+    return FIE_OK;
+}
+
+int fie_sampler_history_write(int32_t* ids, const int64_t* dst, const int32_t* src, int64_t n,
+                              void* stream)
+{
+    if (n < 0 || (n > 0 && (!ids || !dst || !src))) return fail(FIE_E_ARG, "bad history_write arguments");
+    if (n == 0) return FIE_OK;
+    k_history_write<<<(unsigned)((n + 255) / 256), 256, 0, (hipStream_t)stream>>>(ids, dst, src, n);
+    FIE_LAUNCH_CHECK("k_history_write");
     return FIE_OK;
 }
 

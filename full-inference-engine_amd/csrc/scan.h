@@ -116,6 +116,13 @@ FIE_DEV uint4 load_group(const char* rowp, int e0, int V)
     return r;
 }
 
+// End of row `row`'s history in hist_ids: explicit ends (a device-resident history,
+// rows anywhere in one array) or the next CSR offset.
+FIE_DEV int64_t hist_end(const fie_sampler_args& a, int row)
+{
+    return a.hist_ends ? a.hist_ends[row] : a.hist_offsets[row + 1];
+}
+
 // Token idx of a row, as fp32.
 template <int DT>
 FIE_DEV float load_elem(const char* rowp, uint32_t idx)
@@ -201,7 +208,7 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep(const KParams P)
     if (tid < NS) sc[tid] = 0;
     if (tid == 0) { zc = 0; badc = 0; }
     __syncthreads();
-    const int64_t h0 = a.hist_offsets[row], h1 = a.hist_offsets[row + 1];
+    const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
     uint16_t* bk = P.w.bk + (size_t)row * NS * kBucketCap;
     constexpr int kPer = 8;   // ids per thread per batch, loaded together
     for (int64_t base = h0; base < h1; base += (int64_t)kPer * kPrepThreads) {
@@ -304,7 +311,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
             if ((uint32_t)tid < nb) count(e0);
             for (uint32_t i = tid + kScanThreads; i < nb; i += kScanThreads) count(P.w.bk[rs * kBucketCap + i]);
         } else {
-            const int64_t h0 = a.hist_offsets[row], h1 = a.hist_offsets[row + 1];
+            const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
             for (int64_t h = h0 + tid; h < h1; h += kScanThreads) {
                 const uint32_t id = (uint32_t)a.hist_ids[h];
                 if (id != 0 && id >= (uint32_t)slo && id < (uint32_t)shi) count(id - (uint32_t)slo);

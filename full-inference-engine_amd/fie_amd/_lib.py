@@ -39,7 +39,7 @@ class SamplerArgs(ctypes.Structure):
         ("hist_offsets", _vp), ("hist_ids", _vp), ("hist_invalid", _vp),
         ("tokens", _vp), ("status", _vp), ("tk_key", _vp), ("cut_comp", _vp),
         ("row_max", _vp), ("kept_mass", _vp), ("row_mass", _vp), ("chosen_logprob", _vp),
-        ("top_ids", _vp), ("top_logprobs", _vp), ("rng", _vp),
+        ("top_ids", _vp), ("top_logprobs", _vp), ("rng", _vp), ("hist_ends", _vp),
     ]
 
 
@@ -54,7 +54,7 @@ class Workspace(ctypes.Structure):
 EXPORTS = (
     "fie_sampler_workspace_size", "fie_sampler_sample", "fie_sampler_stage",
     "fie_sampler_argmax", "fie_sampler_kept", "fie_sampler_cexp", "fie_sampler_last_error",
-    "fie_sampler_sample_noalloc", "fie_sampler_uniforms",
+    "fie_sampler_sample_noalloc", "fie_sampler_uniforms", "fie_sampler_history_write",
 )
 SCRATCH_BYTES = 64 << 20
 
@@ -96,6 +96,7 @@ def bind(lib) -> None:
     lib.fie_sampler_cexp.argtypes = [_vp, _vp, ctypes.c_int64, _vp]
     lib.fie_sampler_sample_noalloc.argtypes = [ctypes.POINTER(SamplerArgs), _vp]
     lib.fie_sampler_uniforms.argtypes = [_vp, _vp, ctypes.c_int32, _vp]
+    lib.fie_sampler_history_write.argtypes = [_vp, _vp, _vp, ctypes.c_int64, _vp]
     lib.fie_sampler_last_error.restype = ctypes.c_char_p
     for name in EXPORTS:
         if name not in ("fie_sampler_workspace_size", "fie_sampler_last_error"):

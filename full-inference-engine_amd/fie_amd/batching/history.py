@@ -1,0 +1,145 @@
+"""Penalty histories kept on the device across steps.
+
+The reference rebuilds every penalised row's seen-token table on the host at every
+step (engine/batching/sampler.py:134-155): O(rows x context) Python work and a
+fresh upload, although a decoding request's context only grows by one token per
+step (engine/batching/continuous_batching.py:1920-1925 passes prompt + output).
+``DeviceHistory`` keeps each request's context in one device array instead and
+uploads only what was appended since the request's last step; the kernels read
+each row's [start, end) range of that array (``fie_sampler_args.hist_ends``).
+
+A context that is not an extension of the stored one (shorter, or a different
+token where the stored one ends) is stored afresh, so a preempted and rebuilt
+request still samples from exactly the context it passes.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+
+class _Slot:
+    __slots__ = ("start", "cap", "length", "last", "vocab", "bigs", "zero", "late")
+
+    def __init__(self, start: int, cap: int, vocab: int):
+        self.start, self.cap, self.length, self.last, self.vocab = start, cap, 0, -1, vocab
+        self.bigs: set[int] = set()   # distinct ids >= vocab seen
+        self.zero: int | None = None  # position of the first token 0
+        self.late = False             # an id >= vocab first occurs after the first 0
+
+
+class DeviceHistory:
+    """Per-request contexts in one int32 device array (a bump arena)."""
+
+    def __init__(self, device: torch.device, capacity: int = 1 << 20):
+        self.device = device
+        self.ids = torch.empty(capacity, dtype=torch.int32, device=device)
+        self.top = 0
+        self.live = 0
+        self.slots: dict[object, _Slot] = {}
+
+    # ------------------------------------------------------------------ storage
+    def _reserve(self, n: int) -> int:
+        """Start of n free ints, growing (or compacting) the array when full."""
+        if self.top + n <= self.ids.numel():
+            at = self.top
+            self.top += n
+            return at
+        size = max(2 * self.ids.numel(), 2 * (self.live + n))
+        fresh = torch.empty(size, dtype=torch.int32, device=self.device)
+        if self.top - self.live > self.live:
+            # mostly dead space: move the live slots down
+            at = 0
+            for slot in self.slots.values():
+                fresh[at:at + slot.length].copy_(self.ids[slot.start:slot.start + slot.length])
+                slot.start = at
+                at += slot.cap
+            self.top = at
+        else:
+            fresh[:self.top].copy_(self.ids[:self.top])
+        self.ids = fresh
+        at = self.top
+        self.top += n
+        return at
+
+    def _new_slot(self, rid: object, need: int, vocab: int) -> _Slot:
+        old = self.slots.pop(rid, None)
+        if old is not None:
+            self.live -= old.cap
+        cap = max(256, 2 * need)
+        slot = _Slot(self._reserve(cap), cap, vocab)
+        self.slots[rid] = slot
+        self.live += cap
+        return slot
+
+    def _grow(self, slot: _Slot, need: int) -> None:
+        cap = max(2 * slot.cap, 2 * need)
+        start = self._reserve(cap)
+        self.ids[start:start + slot.length].copy_(self.ids[slot.start:slot.start + slot.length])
+        self.live += cap - slot.cap
+        slot.start, slot.cap = start, cap
+
+    def forget(self, request_ids: list[object]) -> None:
+        for rid in request_ids:
+            slot = self.slots.pop(rid, None)
+            if slot is not None:
+                self.live -= slot.cap
+
+    # ------------------------------------------------------------------ one step
+    @staticmethod
+    def _note(slot: _Slot, new: np.ndarray, vocab: int) -> None:
+        """Token-0 bookkeeping of sampler.py:148,156-157 over appended ids."""
+        if not new.size:
+            return
+        zeros = np.nonzero(new == 0)[0]
+        big = np.nonzero(new >= vocab)[0]
+        if slot.zero is None and zeros.size:
+            slot.zero = slot.length + int(zeros[0])
+        for p in big.tolist():
+            t = int(new[p])
+            if t not in slot.bigs:
+                slot.bigs.add(t)
+                if slot.zero is not None and slot.length + p > slot.zero:
+                    slot.late = True
+
+    def update(self, contexts: list[list[int]], include: np.ndarray, request_ids: list[object],
+               vocab: int):
+        """Bring the penalised rows' stored contexts up to date.  Returns (starts,
+        ends, hist_invalid or None, longest, write_dst, write_src): the rows'
+        ranges in ``ids`` and the appended tokens still to be written there."""
+        rows = len(contexts)
+        starts = np.zeros(rows, dtype=np.int64)
+        ends = np.zeros(rows, dtype=np.int64)
+        invalid = np.zeros(rows, dtype=np.int32)
+        longest = 0
+        dst_parts, src_parts = [], []
+        for r in range(rows):
+            if not include[r]:
+                continue
+            ctx = contexts[r]
+            n = len(ctx)
+            rid = request_ids[r]
+            slot = self.slots.get(rid)
+            if (slot is None or slot.vocab != vocab or n < slot.length
+                    or (slot.length and ctx[slot.length - 1] != slot.last)):
+                slot = self._new_slot(rid, n, vocab)
+            elif n > slot.cap:
+                self._grow(slot, n)
+            if n > slot.length:
+                new = np.asarray(ctx[slot.length:], dtype=np.int64)
+                if new.min() < 0 or new.max() >= 2**31:
+                    raise ValueError("penalty context token ids must be in [0, 2**31)")
+                self._note(slot, new, vocab)
+                dst_parts.append(np.arange(slot.start + slot.length, slot.start + n, dtype=np.int64))
+                src_parts.append(new.astype(np.int32))
+                slot.length = n
+                slot.last = int(ctx[-1])
+            starts[r] = slot.start
+            ends[r] = slot.start + n
+            if slot.bigs:
+                invalid[r] = len(slot.bigs) | ((1 << 30) if slot.late else 0)
+            longest = max(longest, n)
+        dst = np.concatenate(dst_parts) if dst_parts else np.zeros(0, np.int64)
+        src = np.concatenate(src_parts) if src_parts else np.zeros(0, np.int32)
+        return starts, ends, (invalid if invalid.any() else None), longest, dst, src

@@ -22,6 +22,7 @@ import numpy as np
 import torch
 
 from ..kernel import FLAG_GREEDY, FLAG_PENALTY, FusedSampler, HostParams
+from .history import DeviceHistory
 from ..runtime.sampling import SamplingParams
 
 
@@ -72,10 +73,14 @@ _EMPTY = np.zeros(0, dtype=np.int64)
 
 
 def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarray | None,
-                   contexts: list[list[int]] | None, rng: np.ndarray | None = None) -> HostParams:
+                   contexts: list[list[int]] | None, rng: np.ndarray | None = None,
+                   history: DeviceHistory | None = None,
+                   request_ids: list[object] | None = None) -> HostParams:
     """Per-row arrays for the kernels, derived the way sampler.py:109,182-192 does.
     The draws are `uniforms` (float64 [rows]) or, when `rng` (uint64 [rows, 3]) is
-    given, derived on the device from it."""
+    given, derived on the device from it.  With a `history` and `request_ids` the
+    penalty contexts are kept on the device across steps (only appended tokens
+    move); otherwise they are packed afresh."""
     rows = len(params)
     if uniforms is None:
         uniforms = np.zeros(rows, dtype=np.float64)
@@ -88,7 +93,11 @@ def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarra
     lp = np.fromiter((-1 if p.logprobs is None else p.logprobs for p in params),
                      dtype=np.int32, count=rows)
     apply = bool(pen.any()) and contexts is not None
-    if apply:
+    ends = dst = src = None
+    if apply and history is not None and request_ids is not None:
+        offsets, ends, invalid, longest, dst, src = history.update(contexts, pen, request_ids, vocab)
+        ids = _EMPTY.astype(np.int32)
+    elif apply:
         offsets, ids, invalid, longest = pack_history(contexts, pen, vocab)
     else:
         offsets, ids, invalid, longest = np.zeros(rows + 1, np.int64), _EMPTY.astype(np.int32), None, 0
@@ -109,6 +118,10 @@ def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarra
         hist_invalid=invalid,
         max_row_hist=longest,
         rng=None if rng is None else np.ascontiguousarray(rng, dtype=np.uint64).reshape(rows, 3),
+        hist_ends=ends,
+        hist_store=history if ends is not None else None,
+        hist_write_dst=dst,
+        hist_write_src=src,
     )
 
 
@@ -139,6 +152,8 @@ class BatchedSampler:
         # not per seed; at most max_generators of them, least recently used dropped.
         self._seeded: OrderedDict[object, int] = OrderedDict()
         self._max_generators = max_generators
+        # Penalty contexts of the requests, kept on the device between steps.
+        self._history = DeviceHistory(self.device)
 
     def _next_draw(self, request_id: object) -> int:
         n = self._seeded.pop(request_id, 0) + 1
@@ -151,6 +166,7 @@ class BatchedSampler:
         """Drop the streams of finished requests (sampler.py:75-78)."""
         for request_id in request_ids:
             self._seeded.pop(request_id, None)
+        self._history.forget(request_ids)
 
     def _draw_keys(self, params: list[SamplingParams],
                    request_ids: list[object] | None) -> np.ndarray:
@@ -198,7 +214,8 @@ class BatchedSampler:
             return SampleResult(self._fused.argmax(logits).tolist(), {})
 
         hp = resolve_params(params, vocab, None, context_tokens,
-                            rng=self._draw_keys(params, request_ids))
+                            rng=self._draw_keys(params, request_ids),
+                            history=self._history, request_ids=request_ids)
         out, _, _ = self._fused.step(logits, hp)
         tokens = [int(t) for t in out["tokens"]]
         return SampleResult(tokens, self._logprobs(params, tokens, out))

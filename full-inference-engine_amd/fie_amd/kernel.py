@@ -68,6 +68,22 @@ class HostParams:
     hist_invalid: np.ndarray | None = None   # int32 [rows], rows with ids >= vocab
     max_row_hist: int = 0
     rng: np.ndarray | None = None            # uint64 [rows, 3]: on-device draws (key0, key1, counter)
+    # A device-resident history (DeviceHistory): hist_off then holds the rows'
+    # starts [rows] and hist_ends their ends in hist_store.ids; hist_write_dst/src
+    # are the appended tokens to write there before the step.
+    hist_ends: np.ndarray | None = None
+    hist_store: object | None = None
+    hist_write_dst: np.ndarray | None = None
+    hist_write_src: np.ndarray | None = None
+
+    def tail_ints(self) -> int:
+        """int32 words of the step block's variable tail: the CSR ids, or the
+        (int64 position, int32 id) pairs of a device-resident history's appends."""
+        if not self.apply_penalties:
+            return 0
+        if self.hist_ends is not None:
+            return 3 * int(self.hist_write_dst.shape[0]) + 2
+        return int(self.hist_off[-1])
 
     @property
     def rows(self) -> int:
@@ -87,6 +103,8 @@ class DeviceStep:
             o = _align(o + max(rows, 1) * width * np.dtype(dt).itemsize)
         offs["hist_off"] = o
         o = _align(o + (rows + 1) * 8)
+        offs["hist_end"] = o
+        o = _align(o + max(rows, 1) * 8)
         offs["hist_ids"] = o
         o = _align(o + max(hist_cap, 1) * 4)
         self.out_begin = o
@@ -113,7 +131,16 @@ class DeviceStep:
             src = getattr(hp, name)
             if src is not None:
                 self.host_view(name, dt, self.rows * width)[:] = np.asarray(src).reshape(-1)
-        self.host_view("hist_off", np.int64, self.rows + 1)[:] = hp.hist_off
+        self.host_view("hist_off", np.int64, len(hp.hist_off))[:] = hp.hist_off
+        if hp.hist_ends is not None:
+            # device-resident history: row ranges, then the appended (position, id) pairs
+            self.host_view("hist_end", np.int64, self.rows)[:] = hp.hist_ends
+            n = int(hp.hist_write_dst.shape[0])
+            o = self.offs["hist_ids"]
+            self.host_np[o:o + 8 * n].view(np.int64)[:] = hp.hist_write_dst
+            self.host_np[o + 8 * n:o + 12 * n].view(np.int32)[:] = hp.hist_write_src
+            self.param_bytes = o + 12 * n
+            return
         n = int(hp.hist_off[-1])
         if n:
             self.host_view("hist_ids", np.int32, n)[:] = hp.hist_ids
@@ -203,6 +230,9 @@ class FusedSampler:
         a.max_row_hist = int(hp.max_row_hist)
         a.repetition, a.presence, a.frequency = buf.ptr("rep"), buf.ptr("pres"), buf.ptr("freq")
         a.hist_offsets, a.hist_ids = buf.ptr("hist_off"), buf.ptr("hist_ids")
+        if hp.hist_ends is not None:
+            a.hist_ends = buf.ptr("hist_end")
+            a.hist_ids = hp.hist_store.ids.data_ptr()
         a.hist_invalid = buf.ptr("hist_invalid") if hp.hist_invalid is not None else None
         a.tokens, a.status, a.tk_key = buf.ptr("tokens"), buf.ptr("status"), buf.ptr("tk_key")
         a.cut_comp, a.row_max = buf.ptr("cut_comp"), buf.ptr("row_max")
@@ -268,11 +298,15 @@ class FusedSampler:
     def step(self, logits: torch.Tensor, hp: HostParams):
         """Upload, launch, download; returns (outputs, args, buffers) after one sync."""
         rows = logits.shape[0]
-        hist_total = int(hp.hist_off[-1]) if hp.apply_penalties else 0
-        buf = self.step_buffers(rows, hist_total)
+        buf = self.step_buffers(rows, hp.tail_ints())
         buf.stage(hp)
         stream = torch.cuda.current_stream(self.device)
         buf.upload(stream)
+        if hp.hist_ends is not None and hp.hist_write_dst.shape[0]:
+            n = int(hp.hist_write_dst.shape[0])
+            o = buf.ptr("hist_ids")
+            _lib.check(self.lib.fie_sampler_history_write(hp.hist_store.ids.data_ptr(), o, o + 8 * n, n,
+                                                          self._stream_ptr()), "fie_sampler_history_write")
         args = self.build_args(logits, buf, hp)
         self.launch(args)
         buf.download(stream)

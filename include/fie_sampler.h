@@ -87,8 +87,9 @@ typedef struct fie_sampler_args {
     const float* repetition;
     const float* presence;
     const float* frequency;
-    const int64_t* hist_offsets;   /* [rows+1] */
-    const int32_t* hist_ids;       /* [hist_offsets[rows]], each id >= 0 */
+    const int64_t* hist_offsets;   /* [rows+1]: row r's ids are hist_ids[offsets[r], offsets[r+1]),
+                                      or [offsets[r], hist_ends[r]) when hist_ends is given */
+    const int32_t* hist_ids;       /* each id >= 0 */
     /* [rows] or NULL.  For a row whose history holds ids >= vocab: the number of
        distinct such ids, plus (1 << 30) if one of them first occurs after the first
        occurrence of token 0.  NULL means no id >= vocab occurs (checked: a row that
@@ -114,6 +115,11 @@ typedef struct fie_sampler_args {
        key (key0, key1), as (x >> 11) * 2^-53, and `uniform` is not read.  The
        caller keeps one key per stream and advances its counter per draw. */
     const uint64_t* rng;
+
+    /* [rows] or NULL: explicit ends of the rows' histories, for a history that
+       lives in one device array across steps (rows in any order, non-contiguous);
+       hist_offsets then holds the starts [rows]. */
+    const int64_t* hist_ends;
 } fie_sampler_args;
 
 /* Device workspace owned by the caller: `bytes` of device memory at `ptr`
@@ -160,6 +166,12 @@ int fie_sampler_kept(const fie_sampler_args* args, uint8_t* kept, float* probs,
 
 /* The build's canonical fp32 exponential on n device values (verification aid). */
 int fie_sampler_cexp(const float* in, float* out, int64_t n, void* stream);
+
+/* ids[dst[i]] = src[i] for i < n: appends new tokens to penalty histories kept in
+   one device array across steps (no counterpart in the reference, whose history is
+   repacked on the host every step, sampler.py:134-155). */
+int fie_sampler_history_write(int32_t* ids, const int64_t* dst, const int32_t* src, int64_t n,
+                              void* stream);
 
 /* The on-device uniforms of `rng` (see fie_sampler_args) for `rows` rows into
    out[rows] (verification; no counterpart in the reference). */

@@ -18,7 +18,7 @@ import torch
 import oracle as O
 from fie_amd import _lib
 from fie_amd import workloads as W
-from fie_amd.batching.sampler import BatchedSampler, resolve_params
+from fie_amd.batching.sampler import SEEDED_STREAM, SHARED_STREAM, BatchedSampler, resolve_params
 from fie_amd.kernel import FusedSampler
 from fie_amd.runtime.sampling import SamplingParams
 
@@ -319,7 +319,6 @@ def test_batched_sampler_draws_on_device_like_the_oracle(fs):
     """BatchedSampler's rows draw on the device from (seed or shared key, stream,
     counter); the oracle, given the same uniforms from numpy's Philox, picks the
     same tokens, over two steps (the counters advance)."""
-    from fie_amd.batching.sampler import SEEDED_STREAM, SHARED_STREAM
     rng = np.random.default_rng(23)
     rows, vocab = 12, 30000
     x = torch.from_numpy(rng.normal(0, 1.5, (rows, vocab)).astype(np.float32)).to(DEV)
@@ -339,6 +338,34 @@ def test_batched_sampler_draws_on_device_like_the_oracle(fs):
                 u.append(_philox_uniform(p.seed, SEEDED_STREAM, step))
         ref = O.canonical_step(x.cpu().numpy(), O.resolve(params, vocab), np.array(u))
         assert res.token_ids == ref.tokens.tolist(), step
+
+
+def test_device_resident_history_over_decode_steps(fs):
+    """BatchedSampler keeps penalty contexts on the device and uploads only the
+    appended tokens: over several decode steps (one token per row, a rebuilt
+    context, ids >= vocab and token 0 for the token-0 rule) its tokens equal the
+    oracle's on the full contexts packed afresh."""
+    rng = np.random.default_rng(31)
+    rows, vocab = 9, 20000
+    x = torch.from_numpy(rng.normal(0, 2.0, (rows, vocab)).astype(np.float32)).half().to(DEV)
+    params = [SamplingParams(temperature=0.9, top_k=(0, 40)[r % 2], top_p=(1.0, 0.9)[r % 3 == 0],
+                             repetition_penalty=1.3, frequency_penalty=0.2, presence_penalty=0.1,
+                             seed=500 + r) for r in range(rows)]
+    ctx = [list(rng.integers(0, vocab, size=int(rng.integers(5, 300)))) for _ in range(rows)]
+    ctx[2] += [0, vocab + 5]
+    ctx[4] = [vocab + 1, 0] + ctx[4]
+    ids = [f"d{r}" for r in range(rows)]
+    s = BatchedSampler(DEV)
+    for step in range(1, 6):
+        if step == 3:
+            ctx[6] = ctx[6][:10]                                          # rebuilt, shorter
+        res = s.sample(x, params, ctx, ids)
+        u = [_philox_uniform(p.seed, SEEDED_STREAM, step) for p in params]
+        ref = O.canonical_step(x.float().cpu().numpy(), O.resolve(params, vocab), np.array(u),
+                               contexts=ctx)
+        assert res.token_ids == ref.tokens.tolist(), step
+        for c, t in zip(ctx, res.token_ids):
+            c.append(t)
 
 
 def test_c_abi_direct_calls_and_errors(fs):

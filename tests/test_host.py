@@ -126,6 +126,46 @@ def test_resolve_params_follows_the_reference_row_rules():
     assert not resolve_params(params, vocab, np.zeros(4), None).apply_penalties
 
 
+def test_device_history_tracks_appends_rebuilds_and_growth():
+    """DeviceHistory's bookkeeping on a CPU array, the appends written as the
+    kernel writes them: after every update each penalised row's [start, end) range
+    holds exactly its context, only appended tokens are written, and the token-0
+    flags equal pack_history's."""
+    import torch
+    from fie_amd.batching.history import DeviceHistory
+
+    vocab = 40
+    h = DeviceHistory(torch.device("cpu"), capacity=300)
+    rng = np.random.default_rng(8)
+    ctx = {f"r{i}": list(rng.integers(0, vocab, size=int(rng.integers(1, 30)))) for i in range(5)}
+    for step in range(60):
+        ids = list(ctx)
+        for rid in ids:
+            ctx[rid].append(int(rng.integers(0, vocab + 3)))           # decode: one token
+        if step % 17 == 5:
+            ctx["r1"] = ctx["r1"][:3] + [7, 7]                         # rebuilt shorter
+        if step % 23 == 11:
+            h.forget(["r2"])
+            ctx["r9"] = list(rng.integers(0, vocab, size=400))         # forces growth
+        ids = list(ctx)
+        include = np.array([rid != "r3" for rid in ids])
+        contexts = [ctx[rid] for rid in ids]
+        starts, ends, invalid, longest, dst, src = h.update(contexts, include, ids, vocab)
+        h.ids[torch.from_numpy(dst)] = torch.from_numpy(src)            # what k_history_write does
+        for r, rid in enumerate(ids):
+            got = h.ids[starts[r]:ends[r]].numpy()
+            if include[r]:
+                np.testing.assert_array_equal(got, np.array(ctx[rid], dtype=np.int32))
+            else:
+                assert starts[r] == ends[r] == 0
+        _, _, want_inv, want_long = pack_history(contexts, include, vocab)
+        np.testing.assert_array_equal(invalid if invalid is not None else 0,
+                                      want_inv if want_inv is not None else 0)
+        assert longest == want_long
+        if step > 0 and step % 17 != 5 and step % 23 != 11:
+            assert dst.size == sum(include)                            # only the appends moved
+
+
 # ---------------------------------------------------------------- the adapter's calls
 class _NoKernels(BatchedSampler):
     """BatchedSampler with its host state only (the constructor's device setup is
@@ -137,6 +177,9 @@ class _NoKernels(BatchedSampler):
         self._shared_draws = 0
         self._seeded = OrderedDict()
         self._max_generators = max_generators
+        import torch
+        from fie_amd.batching.history import DeviceHistory
+        self._history = DeviceHistory(torch.device("cpu"), capacity=16)
 
 
 def test_sample_validation_errors():
