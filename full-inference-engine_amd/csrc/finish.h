@@ -425,7 +425,18 @@ FIE_DEV int dbin_key(float M, uint32_t key)
     return q < (float)(kPassBins - 1) ? (int)q : kPassBins - 1;
 }
 
-FIE_DEV u128 bin_mass(const FinSmem& S, int b) { return ((u128)S.pm_hi[b] << 64) | S.pm_lo[b]; }
+// Bin masses of the d-bins are kept as two 41-bit limbs (w < 2^82): each limb sum
+// over at most 2^19 tokens stays below 2^60, so plain non-returning 64-bit LDS
+// atomics add them exactly, with no carry to detect.
+FIE_DEV u128 bin_mass(const FinSmem& S, int b) { return ((u128)S.pm_hi[b] << 41) + S.pm_lo[b]; }
+
+FIE_DEV void bin_add(FinSmem& S, int b, u128 w)
+{
+    constexpr uint64_t kLimb = (1ull << 41) - 1;
+    const uint64_t lo = (uint64_t)w & kLimb, hi = (uint64_t)(w >> 41);
+    if (lo) atomicAdd((unsigned long long*)&S.pm_lo[b], (unsigned long long)lo);
+    if (hi) atomicAdd((unsigned long long*)&S.pm_hi[b], (unsigned long long)hi);
+}
 
 // Ascending scan of bins [0, bmax], bin bmax measuring `last` instead of its own
 // total, for the bin where the running measure (count, or mass when MASS) first
@@ -495,15 +506,7 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
     row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](uint64_t c) {
         const int b = dbin_key(M, comp_k(c));
         atomicAdd(&S.pc[b], 1u);
-        const u128 w = comp_weight(S, c);
-        const uint64_t lo = (uint64_t)w;
-        if (lo) {
-            const uint64_t old = atomicAdd((unsigned long long*)&S.pm_lo[b], (unsigned long long)lo);
-            const uint64_t hi = (uint64_t)(w >> 64) + ((old + lo < old) ? 1ull : 0ull);
-            if (hi) atomicAdd((unsigned long long*)&S.pm_hi[b], (unsigned long long)hi);
-        } else if ((uint64_t)(w >> 64)) {
-            atomicAdd((unsigned long long*)&S.pm_hi[b], (unsigned long long)(w >> 64));
-        }
+        bin_add(S, b, comp_weight(S, c));
     });
     FIE_MARK(12);
     int cur = -1, ncur = 0;   // the bin held in S.cand, its element count
@@ -626,13 +629,7 @@ FIE_DEV int narrow_candidates(FinSmem& S, int nv, float M, int cnt, bool use_mas
         const uint64_t c = S.cand[i];
         const int b = dbin_key(M, comp_k(c));
         atomicAdd(&S.pc[b], 1u);
-        if (use_mass) {
-            const u128 w = comp_weight(S, c);
-            const uint64_t lo = (uint64_t)w;
-            const uint64_t old = atomicAdd((unsigned long long*)&S.pm_lo[b], (unsigned long long)lo);
-            const uint64_t hi = (uint64_t)(w >> 64) + ((old + lo < old) ? 1ull : 0ull);
-            if (hi) atomicAdd((unsigned long long*)&S.pm_hi[b], (unsigned long long)hi);
-        }
+        if (use_mass) bin_add(S, b, comp_weight(S, c));
     }
     __syncthreads();
     u128 above;
@@ -700,27 +697,39 @@ FIE_DEV bool q1_keeps(FinSmem& S, const KParams& P, int row)
 FIE_DEV int load_candidates(FinSmem& S, const KParams& P, int row, int NT, int n, float s,
                             uint32_t k0, uint32_t safe)
 {
+    constexpr int kPer = 4;                      // candidates per thread per batch
     if (threadIdx.x == 0) { S.n = 0; S.cmax = 0; }
     __syncthreads();
     uint64_t best = 0;
-    for (int i = threadIdx.x; i < n; i += kFinThreads) {
-        uint64_t c;
-        if (i == n - 1) {
-            c = comp_key(k0, 0);
-        } else {
-            int lo = 0, hi = NT - 1;             // tile t with coff[t] <= i < coff[t+1]
-            while (lo < hi) {
-                const int mid = (lo + hi + 1) >> 1;
-                if (S.coff[mid] <= (uint32_t)i) lo = mid;
-                else hi = mid - 1;
+    for (int base = 0; base < n; base += kPer * kFinThreads) {
+        // the tiles of this thread's elements first (LDS), then all their loads in
+        // flight together, then the conversions
+        uint64_t xc[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int i = base + q * kFinThreads + threadIdx.x;
+            xc[q] = 0;
+            if (i < n - 1) {
+                int lo = 0, hi = NT - 1;         // tile t with coff[t] <= i < coff[t+1]
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (S.coff[mid] <= (uint32_t)i) lo = mid;
+                    else hi = mid - 1;
+                }
+                xc[q] = P.w.cand[((size_t)row * NT + lo) * kCapW + (i - S.coff[lo])];
             }
-            const uint64_t xc = P.w.cand[((size_t)row * NT + lo) * kCapW + (i - S.coff[lo])];
-            c = comp_key(fkey(y_of_xkey(comp_k(xc), s)), comp_idx(xc));
         }
-        best = c > best ? c : best;
-        if (comp_k(c) > safe) {
-            const uint32_t at = atomicAdd(&S.n, 1u);
-            if (at < (uint32_t)kGCap) S.cand[at] = c;
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int i = base + q * kFinThreads + threadIdx.x;
+            if (i >= n) continue;
+            const uint64_t c = i == n - 1 ? comp_key(k0, 0)
+                                          : comp_key(fkey(y_of_xkey(comp_k(xc[q]), s)), comp_idx(xc[q]));
+            best = c > best ? c : best;
+            if (comp_k(c) > safe) {
+                const uint32_t at = atomicAdd(&S.n, 1u);
+                if (at < (uint32_t)kGCap) S.cand[at] = c;
+            }
         }
     }
     best = wave_max_u64(best);
@@ -937,14 +946,22 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
     if (pen && P.w.bad[row] && !a.hist_invalid) status |= FIE_ROW_UNCOUNTED_IDS;
 
     FIE_MARK(0);
+    // Every per-tile partial this row reads, loaded together up front: the tile
+    // maxima, sums, candidate counts and bounds, and token 0's logit.
+    const bool need_cand = !greedy || lp > 0;
+    const size_t tbase = (size_t)row * NT + tid;
+    const uint64_t pf_max = tid < NT ? P.w.maxc[tbase] : 0ull;
+    const uint64_t pf_sw = (need_mass && tid < NT) ? P.w.sw[tbase] : 0ull;
+    const uint32_t pf_nc = (need_cand && tid < NT) ? P.w.ncand[tbase] : 0u;
+    const uint32_t pf_bd = (need_cand && tid < NT) ? P.w.bound[tbase] : 0u;
+    const float x0 = P.w.tok0x[row];
     // Tile maxima (x keys) and the row maximum.
-    if (tid < NT) S.tmc[tid] = P.w.maxc[(size_t)row * NT + tid];
+    if (tid < NT) S.tmc[tid] = pf_max;
     __syncthreads();
     const uint64_t xm = block_max_u64<kFinThreads>(tid < NT ? S.tmc[tid] : 0ull, S.red64);
 
     FIE_MARK(1);
     // Token 0 (a tile of its own).
-    const float x0 = P.w.tok0x[row];
     const uint32_t c0 = pen ? P.w.tok0c[row] : 0u;
     float w0 = x0;
     if (c0 && q1_keeps(S, P, row)) w0 = penalize(x0, rep, pres, freq, c0);
@@ -978,7 +995,7 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
     u128 sall = 0;
     if (need_mass) {
         u128 part = 0;
-        if (tid < NT) part = (u128)S.ct[tid + 1] * P.w.sw[(size_t)row * NT + tid];
+        if (tid < NT) part = (u128)S.ct[tid + 1] * pf_sw;
         if (tid == 0) part += (u128)tok_weight(y0, y0) * S.ct[0];
         sall = block_sum_u128<kFinThreads>(part, S.red128);
     }
@@ -1004,14 +1021,14 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
     // Candidates as y-domain composites, sorted, and the safety key: every token
     // whose scaled key exceeds `safe` is among them.
     int n = 0, nv = 0;       // candidates, and those above the safety key (sorted)
+    int nvall = 0;           // nv before narrowing to a prefix
     uint32_t safe = 0;
     uint64_t cmax = 0;       // the largest candidate composite
     bool sorted = false;
-    const bool need_cand = !greedy || lp > 0;
     if (need_cand) {
         // per-tile counts and bounds: one load per thread, a block prefix sum
-        const uint32_t m = tid < NT ? P.w.ncand[(size_t)row * NT + tid] : 0u;
-        const uint32_t b = tid < NT ? P.w.bound[(size_t)row * NT + tid] : 0u;
+        const uint32_t m = pf_nc;
+        const uint32_t b = pf_bd;
         uint32_t total;
         const uint32_t off = block_excl_scan_u32<kFinThreads>(m, S.red32, &total);
         if (tid < NT) S.coff[tid] = off;
@@ -1026,8 +1043,10 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
         else safe = fkey(y_of_xkey(kx, s));
         // only the complete region is ever used: candidates at or below the safety
         // key are dropped before sorting (S.cmax keeps the largest of all)
+        FIE_MARK(12);
         nv = load_candidates(S, P, row, NT, n, s, k0, safe);
         cmax = S.cmax;
+        FIE_MARK(13);
         if (nv > kSortMax) {
             deep = true;
         } else {
@@ -1046,58 +1065,72 @@ __global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
                 else { by_mass = true; g = floor_mul_f64(urow, sall); }
                 if (by_mass && sall == 0) narrow = false;
             }
+            nvall = nv;
             if (narrow && (cnt > 0 || by_mass)) nv = narrow_candidates(S, nv, M, cnt, by_mass, g);
+            FIE_MARK(14);
             sort_desc(S, nv);
             sorted = true;
         }
     }
 
-    // Sampled rows on the sorted candidates: top-k, min-p, S, top-p cut, draw.
+    // Sampled rows on the sorted candidates: top-k, min-p, S, top-p cut, draw.  The
+    // narrowed prefix holds every crossing by construction; should a cut or draw
+    // still miss it, that is not a verdict: every candidate is then loaded and
+    // sorted and the selection runs again.
     FIE_MARK(4);
     if (!greedy && !deep) {
-        uint32_t tk = 0;
-        if (topk > 0) {
-            // the top-k threshold lies in the complete region iff it holds topk
-            if (nv < topk) deep = true;
-            else tk = comp_k(S.cand[topk - 1]);
-        }
-        const uint32_t tmp = minp_key(M, mp);
-        tau = tk > tmp ? tk : tmp;
-        if (!deep && tau != 0 && tau <= safe) deep = true;
-        FIE_MARK(5);
-        if (!deep) {
-            // survivors (key >= tau) and the complete region (key > safe) are
-            // prefixes of the sorted candidates; with tau != 0 the survivors lie in it
-            const int ns = tau != 0 ? sorted_prefix(S, nv, tau, false) : nv;
-            const Chunks ch = chunk_masses(S, nv);
-            const u128 Sv = tau != 0 ? chunk_prefix(S, ch, ns) : sall;
-            FIE_MARK(6);
-            int lim = ns;
-            if (tp < 1.0f) {
-                const u128 thr = ceil_mul_f32(tp, Sv);
-                u128 incl;
-                const int i = chunk_find(S, ch, thr - 1, lim, &incl);
-                if (i < 0) deep = true;
-                else { cut = S.cand[i]; T = incl; lim = i + 1; }
-            } else {
-                T = Sv;
+        for (;;) {
+            const bool partial = nv < nvall;
+            bool miss = false;
+            uint32_t tk = 0;
+            if (topk > 0) {
+                // the top-k threshold lies in the complete region iff it holds topk
+                if (nv < topk) deep = true;
+                else tk = comp_k(S.cand[topk - 1]);
             }
-            FIE_MARK(7);
+            const uint32_t tmp = minp_key(M, mp);
+            tau = tk > tmp ? tk : tmp;
+            if (!deep && tau != 0 && tau <= safe) deep = true;
+            FIE_MARK(5);
             if (!deep) {
-                if (T == 0) {
-                    token = comp_idx(cmax);
-                    tok_comp = cmax;
-                } else {
-                    const u128 g = floor_mul_f64(urow, T);
+                // survivors (key >= tau) and the complete region (key > safe) are
+                // prefixes of the sorted candidates; with tau != 0 the survivors lie in it
+                const int ns = tau != 0 ? sorted_prefix(S, nv, tau, false) : nv;
+                const Chunks ch = chunk_masses(S, nv);
+                const u128 Sv = tau != 0 ? chunk_prefix(S, ch, ns) : sall;
+                FIE_MARK(6);
+                int lim = ns;
+                cut = 0;
+                if (tp < 1.0f) {
+                    const u128 thr = ceil_mul_f32(tp, Sv);
                     u128 incl;
-                    const int i = chunk_find(S, ch, g, lim, &incl);
-                    if (i < 0) deep = true;
-                    else { token = comp_idx(S.cand[i]); tok_comp = S.cand[i]; }
+                    const int i = chunk_find(S, ch, thr - 1, lim, &incl);
+                    if (i < 0) (partial ? miss : deep) = true;
+                    else { cut = S.cand[i]; T = incl; lim = i + 1; }
+                } else {
+                    T = Sv;
+                }
+                FIE_MARK(7);
+                if (!deep && !miss) {
+                    if (T == 0) {
+                        token = comp_idx(cmax);
+                        tok_comp = cmax;
+                    } else {
+                        const u128 g = floor_mul_f64(urow, T);
+                        u128 incl;
+                        const int i = chunk_find(S, ch, g, lim, &incl);
+                        if (i < 0) (partial ? miss : deep) = true;
+                        else { token = comp_idx(S.cand[i]); tok_comp = S.cand[i]; }
+                    }
                 }
             }
+            FIE_MARK(8);
+            if (!deep && !miss && a.tk_key && tid == 0) a.tk_key[row] = tk;
+            if (!miss) break;
+            nv = load_candidates(S, P, row, NT, n, s, k0, safe);
+            nvall = nv;
+            sort_desc(S, nv);
         }
-        FIE_MARK(8);
-        if (!deep && a.tk_key && tid == 0) a.tk_key[row] = tk;
     }
 
     FIE_MARK(9);

@@ -368,6 +368,22 @@ def test_device_resident_history_over_decode_steps(fs):
             c.append(t)
 
 
+def test_cut_and_draw_beyond_the_first_sorted_prefix(fs):
+    """Power-law rows whose top-p cut or plain draw lies hundreds of candidates
+    deep, yet inside the complete region: the sorted prefix must reach it, equal
+    the oracle, and need no full-row path."""
+    rng = np.random.default_rng(41)
+    rows, vocab = 8, 151936
+    ranks = np.argsort(rng.random((rows, vocab)), axis=1)
+    expo = np.array([1.7, 1.75, 1.65, 1.7, 1.7, 1.8, 1.7, 1.72])[:, None]
+    x = torch.from_numpy((-expo * np.log(ranks + 1.0)).astype(np.float32))
+    params = [SamplingParams(temperature=1.0, top_p=0.99)] * 4 + [SamplingParams(temperature=1.0)] * 4
+    u = np.array([0.3, 0.9, 0.5, 0.99, 0.99, 0.995, 0.98, 0.97])
+    out, ref, gk, gp = run_both(fs, x, params, u)
+    check(out, ref, params, gk, gp)
+    assert (out["status"] & 1).sum() == 0, out["status"]
+
+
 def test_c_abi_direct_calls_and_errors(fs):
     lib = _lib.load()
     ws = fs.ensure_workspace(4, 1000)
