@@ -21,16 +21,17 @@ __device__ uint64_t g_fie_prof[8192 * 16];
 #endif
 
 constexpr int kFinThreads = 512;
-constexpr int kGCap = 8192 + 64;   // composites held in LDS (candidates / a gathered bin)
-constexpr int kPassBins = 2048;    // bins of a full-row radix pass
-constexpr int kChunk = 8192;       // tokens per step of a full-row pass
+constexpr int kGCap = 4096;        // composites held in LDS (candidates / a gathered bin)
+constexpr int kPassBins = 1024;    // bins of a full-row radix pass / of the d-bin histogram
+constexpr int kChunk = 4096;       // tokens per step of a full-row pass
 
 // Radix digits over the 64-bit rank composite (key << 32 | ~index): three over the
 // key, then three over the index (bits 31..24 of ~index are constant for V < 2^24).
 struct Digit {
     int shift, bits;
 };
-__device__ constexpr Digit kDigits[6] = {{53, 11}, {42, 11}, {32, 10}, {21, 11}, {10, 11}, {0, 10}};
+constexpr int kLevels = 7;
+__device__ constexpr Digit kDigits[kLevels] = {{54, 10}, {44, 10}, {34, 10}, {24, 10}, {14, 10}, {4, 10}, {0, 4}};
 
 struct SelResult {
     uint64_t comp;       // the element where the running measure crosses the target
@@ -360,7 +361,7 @@ FIE_DEV SelResult row_select(FinSmem& S, const KParams& P, int row, float s, boo
 {
     uint64_t hiprefix = 0;
     u128 excl = 0;
-    for (int level = 0; level < 6; ++level) {
+    for (int level = 0; level < kLevels; ++level) {
         const Digit dg = kDigits[level];
         if (!(level == 0 && have_l1))
             pass_hist<DT, VEC, MASS>(S, P, row, s, pen, rep, pres, freq, k0, pr, level, hiprefix);
@@ -414,8 +415,8 @@ FIE_DEV uint32_t minp_key(float M, float mp)
 }
 
 // ---------------------------------------------------------------- binned full-row path
-// Bins of a row by d = fl(M - y) at kDQ bins per unit (the last bin takes d >= 32
-// and NaN).  fl(M - y) and the scaling by a power of two are monotone, so bins lie
+// Bins of a row by d = fl(M - y) at kDQ bins per unit (the last bin takes
+// d >= (kPassBins - 1) / kDQ and NaN).  fl(M - y) and the scaling by a power of two are monotone, so bins lie
 // in rule R2 order: a lower bin holds only larger values, and ties share a bin.
 constexpr float kDQ = 64.0f;
 
@@ -741,7 +742,7 @@ FIE_DEV int load_candidates(FinSmem& S, const KParams& P, int row, int NT, int n
 }
 
 // ---------------------------------------------------------------- sorted candidates
-constexpr int kSortMax = 8192;     // candidates sorted in LDS, at most
+constexpr int kSortMax = kGCap;    // candidates sorted in LDS, at most
 
 // v of lane (lane ^ J): DPP moves inside rows of 16 lanes (quad permutes for 1 and
 // 2, row shifts by 4 and 8 selected by the lane's bit), a swizzle inside 32 lanes
@@ -924,7 +925,7 @@ FIE_DEV u128 chunk_prefix(FinSmem& S, const Chunks& ch, int m)
 
 // ---------------------------------------------------------------- k_finish
 template <int DT, bool VEC>
-__global__ __launch_bounds__(kFinThreads) void k_finish(const KParams P)
+__global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
 {
     __shared__ FinSmem S;
     const fie_sampler_args& a = P.a;
