@@ -79,10 +79,11 @@ struct Pred {
     uint32_t tau;
     uint32_t safe;   // 0 = no restriction (keys are never 0)
     uint64_t cut;
+    uint64_t hi = ~0ull;   // composites above hi excluded (none by default)
     FIE_DEV bool operator()(uint64_t c) const
     {
         const uint32_t k = comp_k(c);
-        return k >= tau && k > safe && c >= cut;
+        return k >= tau && k > safe && c >= cut && c <= hi;
     }
 };
 
@@ -510,30 +511,40 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
         bin_add(S, b, comp_weight(S, c));
     });
     FIE_MARK(12);
-    int cur = -1, ncur = 0;   // the bin held in S.cand, its element count
-    auto gather = [&](int b) -> bool {
-        if (b == cur) return true;
-        if (S.pc[b] > (uint32_t)kGCap) return false;
+    // S.cand holds the elements (ncur of them) of bins [cur_lo, cur_hi] and, when
+    // cur2_lo >= 0, of bins [cur2_lo, cur2_hi] as well.
+    int cur_lo = -1, cur_hi = -1, cur2_lo = -1, cur2_hi = -1, ncur = 0;
+    auto gather2 = [&](int bl, int bh, int b2l, int b2h) -> bool {
+        if (bl == cur_lo && bh == cur_hi && b2l == cur2_lo && b2h == cur2_hi) return true;
+        uint32_t cnt = 0;
+        for (int b = bl; b <= bh; ++b) cnt += S.pc[b];
+        for (int b = b2l; b2l >= 0 && b <= b2h; ++b) cnt += S.pc[b];
+        if (cnt > (uint32_t)kGCap) return false;
         if (tid == 0) S.n = 0;
         __syncthreads();
         row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](uint64_t c) {
-            if (dbin_key(M, comp_k(c)) == b) {
+            const int b = dbin_key(M, comp_k(c));
+            if ((b >= bl && b <= bh) || (b2l >= 0 && b >= b2l && b <= b2h)) {
                 const uint32_t at = atomicAdd(&S.n, 1u);
                 if (at < (uint32_t)kGCap) S.cand[at] = c;
             }
         });
         ncur = (int)S.n;
-        cur = b;
+        cur_lo = bl;
+        cur_hi = bh;
+        cur2_lo = b2l;
+        cur2_hi = b2h;
         __syncthreads();
         return true;
     };
+    auto gather = [&](int bl, int bh) -> bool { return gather2(bl, bh, -1, -1); };
 
     // top-k threshold: the element of rank topk - 1
     uint32_t tk = 0;
     if (topk > 0) {
         u128 above;
         const int b = dbin_pick<false>(S, kPassBins - 1, (u128)S.pc[kPassBins - 1], (u128)(topk - 1), &above);
-        if (b < 0 || !gather(b)) return false;
+        if (b < 0 || !gather(b, b)) return false;
         const SelResult r = lds_select<false>(S, ncur, Pred{0, 0, 0}, (u128)(topk - 1) - above);
         if (!r.found) return false;
         tk = comp_k(r.comp);
@@ -547,24 +558,25 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
     u128 Sv = sall;
     if (tau != 0) {
         bt = dbin_key(M, tau);
-        if (!gather(bt)) return false;
+        if (!gather(bt, bt)) return false;
         u128 part = 0;
         for (int i = tid; i < ncur; i += kFinThreads)
             if (comp_k(S.cand[i]) >= tau) part += comp_weight(S, S.cand[i]);
-        for (int b = tid; b < bt; b += kFinThreads) part += bin_mass(S, b);
         lastt = block_sum_u128<kFinThreads>(part, S.red128);
-        Sv = lastt;
-        // lastt so far holds the survivors' whole mass: take the bins before bt out
         u128 before = 0;
         for (int b = tid; b < bt; b += kFinThreads) before += bin_mass(S, b);
-        lastt -= block_sum_u128<kFinThreads>(before, S.red128);
+        Sv = lastt + block_sum_u128<kFinThreads>(before, S.red128);
     }
 
-    // top-p cut among the survivors
+    // top-p cut among the survivors.  The cut's bin b fixes T to (above, above +
+    // m_b], hence the draw t = floor(u T) to a short run of bins [dl, dh]; the pass
+    // that gathers b gathers that run too when it fits.
     uint64_t cut = 0;
     u128 T = Sv;
     int bc = bt;
     u128 lastc = lastt;
+    int dl = -1, dh = -1;     // the draw's run of bins, gathered with the cut's
+    u128 above_dl = 0;        // survivors' mass before bin dl
     if (tp < 1.0f) {
         const u128 thr = ceil_mul_f32(tp, Sv);
         u128 above;
@@ -572,10 +584,31 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
         if (b < 0) {
             T = above;                            // every survivor; no cut (Sv == 0)
         } else {
-            if (!gather(b)) return false;
-            FIE_MARK(13);
-            const SelResult r = lds_select<true>(S, ncur, Pred{tau, 0, 0}, thr - 1 - above);
-            FIE_MARK(14);
+            const u128 mb = b == bt ? lastt : bin_mass(S, b);
+            u128 a2, a3;
+            dl = dbin_pick<true>(S, b, mb, floor_mul_f64(u, above + 1), &a2);
+            dh = dbin_pick<true>(S, b, mb, floor_mul_f64(u, above + mb), &a3);
+            above_dl = a2;
+            if (dl < 0 || dh < 0 || dh >= b || !gather2(b, b, dl, dh)) {
+                dl = dh = -1;
+                if (!gather(b, b)) return false;
+            }
+            // within bin b only: composites of the lower bins (the draw's run) are larger
+            uint64_t chi = ~0ull;
+            if (dl >= 0) {
+                uint64_t mn = ~0ull;
+                for (int i = tid; i < ncur; i += kFinThreads)
+                    if (dbin_key(M, comp_k(S.cand[i])) < b) mn = S.cand[i] < mn ? S.cand[i] : mn;
+                mn = ~wave_max_u64(~mn);
+                if ((tid & 63) == 0) S.red64[tid >> 6] = mn;
+                __syncthreads();
+                for (int w = 0; w < kFinThreads / 64; ++w) mn = S.red64[w] < mn ? S.red64[w] : mn;
+                __syncthreads();
+                chi = mn - 1;
+            }
+            Pred pc{tau, 0, 0};
+            pc.hi = chi;
+            const SelResult r = lds_select<true>(S, ncur, pc, thr - 1 - above);
             if (!r.found) return false;
             cut = r.comp;
             T = above + r.excl + r.meas;
@@ -589,7 +622,7 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
     if (T == 0) {
         u128 above;
         const int b = dbin_pick<false>(S, kPassBins - 1, (u128)S.pc[kPassBins - 1], 0, &above);
-        if (b < 0 || !gather(b)) return false;
+        if (b < 0 || !gather(b, b)) return false;
         const SelResult r = lds_select<false>(S, ncur, Pred{0, 0, 0}, 0);
         if (!r.found) return false;
         tok = r.comp;
@@ -597,9 +630,27 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
         const u128 g = floor_mul_f64(u, T);
         u128 above;
         const int b = dbin_pick<true>(S, bc, lastc, g, &above);
-        if (b < 0 || !gather(b)) return false;
-        FIE_MARK(15);
-        const SelResult r = lds_select<true>(S, ncur, Pred{tau, 0, cut}, g - above);
+        if (b < 0) return false;
+        Pred pd{tau, 0, cut};
+        u128 base = above;
+        if (dl >= 0 && b >= dl && b <= dh) {
+            base = above_dl;                      // the held run [dl, dh]: its elements rank first
+        } else {
+            if (!(b == cur_lo && b == cur_hi) && !gather(b, b)) return false;
+            if (cur2_lo >= 0) {
+                // bin b held below the run: skip the run's (larger) composites
+                uint64_t mn = ~0ull;
+                for (int i = tid; i < ncur; i += kFinThreads)
+                    if (dbin_key(M, comp_k(S.cand[i])) < b) mn = S.cand[i] < mn ? S.cand[i] : mn;
+                mn = ~wave_max_u64(~mn);
+                if ((tid & 63) == 0) S.red64[tid >> 6] = mn;
+                __syncthreads();
+                for (int w = 0; w < kFinThreads / 64; ++w) mn = S.red64[w] < mn ? S.red64[w] : mn;
+                __syncthreads();
+                pd.hi = mn - 1;
+            }
+        }
+        const SelResult r = lds_select<true>(S, ncur, pd, g - base);
         if (!r.found) return false;
         tok = r.comp;
     }
