@@ -64,12 +64,15 @@ struct FinSmem {
 };
 
 // Weight of a y-domain composite under rule R1: floor(cexp(y - m_t) 2^40) * C_t.
+FIE_DEV u128 weight_of(const FinSmem& S, float y, uint32_t idx)
+{
+    const int slot = idx == 0 ? 0 : 1 + (int)(idx / kTile);
+    return (u128)tok_weight(y, S.mt[slot]) * S.ct[slot];
+}
+
 FIE_DEV u128 comp_weight(const FinSmem& S, uint64_t c)
 {
-    const uint32_t idx = comp_idx(c);
-    const int slot = idx == 0 ? 0 : 1 + (int)(idx / kTile);
-    const float y = key_to_float(comp_k(c));
-    return (u128)tok_weight(y, S.mt[slot]) * S.ct[slot];
+    return weight_of(S, key_to_float(comp_k(c)), comp_idx(c));
 }
 
 // Predicate shared by every selection: the element survives top-k / min-p (key >=
@@ -203,8 +206,8 @@ FIE_DEV void recount(FinSmem& S, const fie_sampler_args& a, int row, int lo, int
     __syncthreads();
 }
 
-// Visit every token of the row once, re-reading it from memory: f(comp) with the
-// y-domain composite of each token (token 0 with its settled value y0).  The next
+// Visit every token of the row once, re-reading it from memory: f(y, idx) with each
+// token's scaled (penalised) logit, token 0 with its settled value.  The next
 // chunk's loads are in flight while a chunk is processed; a penalised row counts
 // its chunk's history first, so those loads never wait behind the prefetch.
 template <int DT, bool VEC, class F>
@@ -218,7 +221,7 @@ FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, 
     const char* rowp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * SZ;
     const bool mark = s != 1.0f && s >= 0x1p-30f && s <= 0x1p30f;
     const float rs = 1.0f / s;
-    if (tid == 0 && k0) f(comp_key(k0, 0));
+    if (tid == 0 && k0) f(key_to_float(k0), 0u);
     uint4 cur[NL], nxt[NL];
 #pragma unroll
     for (int j = 0; j < NL; ++j) cur[j] = load_group<DT, VEC>(rowp, (j * kFinThreads + tid) * EPL, V);
@@ -245,7 +248,7 @@ FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, 
                 if (s == 1.0f) y = x + 0.0f;
                 else if (mark && markstein_ok(x)) y = div_markstein(x, s, rs) + 0.0f;
                 else y = scaled(x, s);
-                f(comp_key(fkey(y), (uint32_t)idx));
+                f(y, (uint32_t)idx);
             }
         }
         if (pen) __syncthreads();
@@ -270,7 +273,8 @@ FIE_DEV void pass_hist(FinSmem& S, const KParams& P, int row, float s, bool pen,
         if (MASS) { S.pm_lo[i] = 0; S.pm_hi[i] = 0; }
     }
     __syncthreads();
-    row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](uint64_t c) {
+    row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](float y, uint32_t idx) {
+        const uint64_t c = comp_key(fkey(y), idx);
         if ((top >= 64 || (c >> top) == hiprefix) && pr(c)) {
             const uint32_t d = (uint32_t)(c >> dg.shift) & dmask;
             atomicAdd(&S.pc[d], 1u);
@@ -340,7 +344,8 @@ FIE_DEV int pass_gather(FinSmem& S, const KParams& P, int row, float s, bool pen
 {
     if (threadIdx.x == 0) S.n = 0;
     __syncthreads();
-    row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](uint64_t c) {
+    row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](float y, uint32_t idx) {
+        const uint64_t c = comp_key(fkey(y), idx);
         if ((top >= 64 || (c >> top) == hiprefix) && pr(c)) {
             const uint32_t at = atomicAdd(&S.n, 1u);
             if (at < (uint32_t)kGCap) S.cand[at] = c;
@@ -421,11 +426,13 @@ FIE_DEV uint32_t minp_key(float M, float mp)
 // in rule R2 order: a lower bin holds only larger values, and ties share a bin.
 constexpr float kDQ = 64.0f;
 
-FIE_DEV int dbin_key(float M, uint32_t key)
+FIE_DEV int dbin_y(float M, float y)
 {
-    const float q = (M - key_to_float(key)) * kDQ;
+    const float q = (M - y) * kDQ;
     return q < (float)(kPassBins - 1) ? (int)q : kPassBins - 1;
 }
+
+FIE_DEV int dbin_key(float M, uint32_t key) { return dbin_y(M, key_to_float(key)); }
 
 // Bin masses of the d-bins are kept as two 41-bit limbs (w < 2^82): each limb sum
 // over at most 2^19 tokens stays below 2^60, so plain non-returning 64-bit LDS
@@ -505,10 +512,10 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
         S.pm_hi[i] = 0;
     }
     __syncthreads();
-    row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](uint64_t c) {
-        const int b = dbin_key(M, comp_k(c));
+    row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](float y, uint32_t idx) {
+        const int b = dbin_y(M, y);
         atomicAdd(&S.pc[b], 1u);
-        bin_add(S, b, comp_weight(S, c));
+        bin_add(S, b, weight_of(S, y, idx));
     });
     FIE_MARK(12);
     // S.cand holds the elements (ncur of them) of bins [cur_lo, cur_hi] and, when
@@ -522,11 +529,11 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
         if (cnt > (uint32_t)kGCap) return false;
         if (tid == 0) S.n = 0;
         __syncthreads();
-        row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](uint64_t c) {
-            const int b = dbin_key(M, comp_k(c));
+        row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](float y, uint32_t idx) {
+            const int b = dbin_y(M, y);
             if ((b >= bl && b <= bh) || (b2l >= 0 && b >= b2l && b <= b2h)) {
                 const uint32_t at = atomicAdd(&S.n, 1u);
-                if (at < (uint32_t)kGCap) S.cand[at] = c;
+                if (at < (uint32_t)kGCap) S.cand[at] = comp_key(fkey(y), idx);
             }
         });
         ncur = (int)S.n;
