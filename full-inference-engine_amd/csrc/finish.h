@@ -16,7 +16,10 @@ namespace fie {
 #ifdef FIE_PHASE_PROFILE
 __device__ uint64_t g_fie_prof[8192 * 16];
 #define FIE_MARK(i) do { if (threadIdx.x == 0 && blockIdx.x < 8192) g_fie_prof[(size_t)blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memtime(); } while (0)
+__device__ uint32_t g_fie_why[8192 * 4];
+#define FIE_WHY(k, v) do { if (threadIdx.x == 0 && blockIdx.x < 8192) g_fie_why[(size_t)blockIdx.x * 4 + (k)] = (v); } while (0)
 #else
+#define FIE_WHY(k, v) do { } while (0)
 #define FIE_MARK(i) do { } while (0)
 #endif
 
@@ -1106,6 +1109,8 @@ __global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
         nv = load_candidates(S, P, row, NT, n, s, k0, safe);
         cmax = S.cmax;
         FIE_MARK(13);
+        FIE_WHY(0, (uint32_t)nv);
+        FIE_WHY(1, (uint32_t)n);
         if (nv > kSortMax) {
             deep = true;
         } else {
@@ -1164,7 +1169,7 @@ __global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
                     const u128 thr = ceil_mul_f32(tp, Sv);
                     u128 incl;
                     const int i = chunk_find(S, ch, thr - 1, lim, &incl);
-                    if (i < 0) (partial ? miss : deep) = true;
+                    if (i < 0) { (partial ? miss : deep) = true; FIE_WHY(2, 100 + (uint32_t)partial); FIE_WHY(3, (uint32_t)nv); }
                     else { cut = S.cand[i]; T = incl; lim = i + 1; }
                 } else {
                     T = Sv;
@@ -1178,7 +1183,7 @@ __global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
                         const u128 g = floor_mul_f64(urow, T);
                         u128 incl;
                         const int i = chunk_find(S, ch, g, lim, &incl);
-                        if (i < 0) (partial ? miss : deep) = true;
+                        if (i < 0) { (partial ? miss : deep) = true; FIE_WHY(2, 200 + (uint32_t)partial); FIE_WHY(3, (uint32_t)nv); }
                         else { token = comp_idx(S.cand[i]); tok_comp = S.cand[i]; }
                     }
                 }

@@ -27,8 +27,10 @@ constexpr int kWavesPerWG = kScanThreads / 64;
 constexpr int kSpan = kTile * kWavesPerWG;       // tokens per workgroup (8192)
 constexpr int kEPT = kTile / 64;                 // tokens per lane (32)
 constexpr int kCapW = 64;                        // candidates per tile, at most
-constexpr int kCandMin = 16;                     // candidates per tile for rows without top-k
 constexpr int kStageW = 256;                     // tokens at or above a tile's floor, staged
+constexpr int kCandMin = 16;                     // candidates per tile of greedy rows
+constexpr int kCandWide = kStageW / 8;           // ... of sampled rows without top-k (8 tokens a group)
+constexpr int kCandRow = 4000;                   // ... times the tiles of a row, at most
 constexpr int kMaxTiles = 256;                   // vocab <= 256 * 2048
 constexpr int kBucketCap = 512;                  // history ids of one span held by k_prep
 constexpr int kMaxSpans = kMaxTiles / kWavesPerWG;
@@ -154,10 +156,17 @@ FIE_DEV float y_of_xkey(uint32_t k, float s)
 
 // Candidates per tile a row asks for: enough that the union over tiles holds the
 // row's top-k when the top tokens spread about evenly, at least kCandMin.
-FIE_DEV uint32_t cand_target(int topk, int NT)
+FIE_DEV uint32_t cand_target(int topk, int NT, bool greedy)
 {
-    int c = kCandMin;
-    if (topk > 0) c = 2 * ((topk + NT - 1) / NT) + 4;
+    int c = kCandMin;                              // greedy rows: their top logprobs
+    if (topk > 0) {
+        c = 2 * ((topk + NT - 1) / NT) + 4;
+    } else if (!greedy) {
+        // a top-p cut, min-p or a plain draw: as deep as the finish kernel can sort
+        // (penalties on the chosen tokens flatten a row step after step)
+        c = kCandWide;
+        if (c * NT > kCandRow) c = kCandRow / NT;
+    }
     return (uint32_t)(c < 8 ? 8 : (c < kCapW ? c : kCapW));
 }
 
@@ -474,16 +483,24 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
         if (lane == 0) P.w.sw[slot] = tot;
     }
 
-    // 6. The tile's top tokens.  The floor is the largest 12-bit key prefix with
+    // 6. The tile's top tokens.  The floor is the largest 12- or 20-bit key prefix with
     //    at least c group maxima at or above it, so at least c tokens are; tokens
     //    at or above it are staged in LDS, and when more than kCapW are, the c-th
     //    largest staged key is found by a full-width ballot select.
     if (need_cand) {
-        const uint32_t c = cand_target(topk, NT);
+        // a partial last tile asks for at most half its groups: every group at or
+        // above the floor may stage all its EPL tokens
+        uint32_t c = cand_target(topk, NT, greedy);
+        const int valid = V - lo < kTile ? V - lo : kTile;
+        const uint32_t half = (uint32_t)((valid + EPL - 1) / EPL / 2);
+        if (c > half) c = half > 8u ? half : 8u;
         uint32_t gk[NG];
 #pragma unroll
         for (int g = 0; g < NG; ++g) gk[g] = gm[g] == gm[g] ? fkey(gm[g] + 0.0f) : 0u;
-        const uint32_t floor_key = ballot_select(gk, c, 0u, 31, 20);
+        // a 12-bit prefix for small c; a 20-bit one for wide rows, whose floor
+        // bucket would otherwise hold more group maxima than staging can take
+        const uint32_t floor_key = c > (uint32_t)kCandMin ? ballot_select(gk, c, 0u, 31, 12)
+                                                          : ballot_select(gk, c, 0u, 31, 20);
         // stage: per lane, its tokens at or above the floor, by a float compare
         // against the floor's value (NaN fails it); a floor whose value is not a
         // number (a key of the NaN range) or 0 (all tokens) compares by key instead
@@ -520,13 +537,16 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
             }
         }
         wave_lds_sync();
+        // at most `cap` emitted per tile (ties at the c-th key beyond it stay
+        // below the bound)
+        const uint32_t cap = (uint32_t)kCapW;
         uint32_t bound = floor_key ? floor_key : 1u;
         if (E > (uint32_t)kStageW) {
             // more than kStageW tokens in the floor's bin (massive ties): emit
             // nothing and mark the tile incomplete; the row takes the full-row path
             bound = 0xFFFFFFFFu;
             E = 0;
-        } else if (E > (uint32_t)kCapW) {
+        } else if (E > cap) {
             constexpr int SPL = kStageW / 64;
             uint32_t sk[SPL];
 #pragma unroll
@@ -541,9 +561,9 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
             uint32_t ge = 0;
 #pragma unroll
             for (int q = 0; q < SPL; ++q) ge += popc64(__ballot(sk[q] >= K));
-            bound = ge <= (uint32_t)kCapW ? K : K + 1u;       // ties beyond kCapW dropped
+            bound = ge <= cap ? K : K + 1u;                   // ties beyond cap dropped
         }
-        // emit the staged tokens with key >= bound (at most kCapW)
+        // emit the staged tokens with key >= bound (at most cap)
         uint64_t* out = P.w.cand + slot * kCapW;
         uint32_t nout = 0;
         for (uint32_t q0 = 0; q0 < E; q0 += 64) {
@@ -552,14 +572,14 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
             const bool keep = idx < E && comp_k(cc) >= bound;
             const uint64_t bal = __ballot(keep);
             const uint32_t pos = nout + popc64(bal & ((1ull << lane) - 1));
-            if (keep && pos < (uint32_t)kCapW) out[pos] = cc;   // bound keeps pos < kCapW
+            if (keep && pos < cap) out[pos] = cc;                // bound keeps pos < cap
             nout += popc64(bal);
         }
         if (lane == 0) {
-            // more than kCapW at or above the bound cannot happen (the bound is the
-            // c-th largest staged key, c <= kCapW); should it, the tile reports
+            // more than cap at or above the bound cannot happen (the bound is the
+            // c-th largest staged key, c <= cap); should it, the tile reports
             // itself incomplete and the row takes the full-row path
-            const bool over = nout > (uint32_t)kCapW;
+            const bool over = nout > cap;
             P.w.ncand[slot] = over ? 0u : nout;
             P.w.bound[slot] = over ? 0xFFFFFFFFu : bound;
         }
