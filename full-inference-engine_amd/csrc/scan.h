@@ -213,11 +213,13 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep(const KParams P)
     const fie_sampler_args& a = P.a;
     const int row = blockIdx.x, tid = threadIdx.x, NS = P.NS;
     const uint32_t V = (uint32_t)a.vocab;
-    if (!(a.apply_penalties && (a.flags[row] & FIE_FLAG_PENALTY))) return;
+    // the row's flags and history range are loaded together (one round trip)
+    const int32_t fl = a.flags[row];
+    const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
+    if (!(a.apply_penalties && (fl & FIE_FLAG_PENALTY))) return;
     if (tid < NS) sc[tid] = 0;
     if (tid == 0) { zc = 0; badc = 0; }
     __syncthreads();
-    const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
     uint16_t* bk = P.w.bk + (size_t)row * NS * kBucketCap;
     constexpr int kPer = 8;   // ids per thread per batch, loaded together
     for (int64_t base = h0; base < h1; base += (int64_t)kPer * kPrepThreads) {
@@ -370,9 +372,11 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
                 if (!(markstein_ok(x[i]) || x[i] == 0.0f || !__builtin_isfinite(x[i]))) odd = true;
             }
         } else if (__ballot(mine != 0) != 0) {
+            // a set bit ORs a quiet NaN's exponent and quiet bit into the value
 #pragma unroll
             for (int i = 0; i < kEPT; ++i)
-                if ((mine >> i) & 1u) x[i] = __builtin_nanf("");
+                x[i] = __int_as_float(__float_as_int(x[i]) |
+                                      (__builtin_amdgcn_sbfe((int)mine, (unsigned)i, 1u) & 0x7FC00000));
             uint32_t b = mine;
 #pragma unroll
             for (int q = 0; q < kPS; ++q) {
