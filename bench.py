@@ -2,8 +2,8 @@
 
 One step = one fused sampler call (penalties, temperature, top-k / top-p / min-p,
 draw, logprobs) over one [B, V] logits batch already resident in HBM, with the
-step's parameters and penalty histories resident too: the two kernels k_scan and
-k_finish.  Logits rotate through enough distinct buffers (> 512 MB) that the 256 MB
+step's parameters and penalty histories resident too: the three kernels k_prep,
+k_scan and k_finish.  Logits rotate through enough distinct buffers (> 512 MB) that the 256 MB
 Infinity Cache cannot serve them.
 
 Prints one JSON line: rows/s and us/step for the headline config, the roofline of
@@ -54,6 +54,21 @@ def cpu_model() -> str:
     except OSError:
         pass
     return platform.processor() or "unknown"
+
+
+def measured_traffic(kernel: str, config: int):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary (scaled by the copy calibration it states), or None."""
+    path = os.path.join(_REPO, "profiles", f"k_scan_C{config}_hbm_traffic.md")
+    try:
+        with open(path, encoding="utf-8") as f:
+            for line in f:
+                cells = [c.strip() for c in line.strip().strip("|").split("|")]
+                if len(cells) == 6 and cells[0] == f"`{kernel}`":
+                    return round((float(cells[4]) + float(cells[5])) * 1e6)
+    except (OSError, ValueError):
+        pass
+    return None
 
 
 def algorithmic_bytes(w, hp) -> dict:
@@ -255,7 +270,8 @@ def main() -> None:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
-            "traffic": None,
+            "traffic": measured_traffic(dom, a.config),
+            "traffic_source": f"profiles/k_scan_C{a.config}_hbm_traffic.md (rocprofv3 --pmc, scaled)",
             "algorithmic_bytes": dom_bytes,
         },
         "step_roofline": {"achieved": step_gbs, "frac": step_gbs / HBM_PEAK_GBS,
