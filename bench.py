@@ -29,7 +29,7 @@ sys.path.insert(0, os.path.join(_REPO, "full-inference-engine_amd"))
 
 METRIC = "rows/s + µs per sampler step at B=256,V=152k; % of HBM roofline"
 HBM_PEAK_GBS = 8000.0
-STAGES = ("k_prep", "k_scan", "k_finish")   # fie_sampler_stage 0, 1, 2
+STAGES = ("k_prep", "k_scan", "k_finish", "k_deep")   # fie_sampler_stage 0, 1, 2, 3
 
 
 def parse():

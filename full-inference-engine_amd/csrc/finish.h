@@ -15,9 +15,9 @@ namespace fie {
 
 #ifdef FIE_PHASE_PROFILE
 __device__ uint64_t g_fie_prof[8192 * 16];
-#define FIE_MARK(i) do { if (threadIdx.x == 0 && blockIdx.x < 8192) g_fie_prof[(size_t)blockIdx.x * 16 + (i)] = __builtin_amdgcn_s_memtime(); } while (0)
+#define FIE_MARK(i) do { if (threadIdx.x == 0 && row < 8192) g_fie_prof[(size_t)row * 16 + (i)] = __builtin_amdgcn_s_memtime(); } while (0)
 __device__ uint32_t g_fie_why[8192 * 4];
-#define FIE_WHY(k, v) do { if (threadIdx.x == 0 && blockIdx.x < 8192) g_fie_why[(size_t)blockIdx.x * 4 + (k)] = (v); } while (0)
+#define FIE_WHY(k, v) do { if (threadIdx.x == 0 && row < 8192) g_fie_why[(size_t)row * 4 + (k)] = (v); } while (0)
 #else
 #define FIE_WHY(k, v) do { } while (0)
 #define FIE_MARK(i) do { } while (0)
@@ -48,6 +48,7 @@ struct FinSmem {
     uint32_t pc[kPassBins];                     // full-row pass: counts per bin
     uint64_t pm_lo[kPassBins], pm_hi[kPassBins];// full-row pass: mass per bin
     uint32_t cnt[kChunk];                       // penalty counts of one chunk
+    uint32_t snb[kMaxSpans];                    // history ids per span (k_prep), of a pass's row
     uint32_t hc[256];                           // LDS selection: counts per digit
     uint64_t hm_lo[256], hm_hi[256];            // LDS selection: mass per digit
     float mt[kMaxTiles + 1];                    // tile maxima of y (slot 0 = token 0)
@@ -194,47 +195,65 @@ FIE_DEV SelResult lds_select(FinSmem& S, int n, const Pred pr, u128 g)
 }
 
 // ---------------------------------------------------------------- full-row passes
-// Penalty counts of tokens [lo, hi) of `row` into S.cnt (one u32 per token).
-FIE_DEV void recount(FinSmem& S, const fie_sampler_args& a, int row, int lo, int hi)
-{
-    for (int i = threadIdx.x; i < kChunk; i += kFinThreads) S.cnt[i] = 0;
-    __syncthreads();
-    const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
-    for (int64_t h = h0 + threadIdx.x; h < h1; h += kFinThreads) {
-        const uint32_t id = (uint32_t)a.hist_ids[h];
-        if (id >= (uint32_t)lo && id < (uint32_t)hi && id != 0) {
-            atomicAdd(&S.cnt[id - lo], 1u);
-        }
-    }
-    __syncthreads();
-}
-
 // Visit every token of the row once, re-reading it from memory: f(y, idx) with each
-// token's scaled (penalised) logit, token 0 with its settled value.  The next
-// chunk's loads are in flight while a chunk is processed; a penalised row counts
-// its chunk's history first, so those loads never wait behind the prefetch.
+// token's scaled (penalised) logit, token 0 with its settled value.  The row streams
+// in kChunk-token chunks, the next chunk's loads in flight while one is processed
+// (a pass is bound by its per-token instructions: deeper prefetch measured no
+// faster).  A penalised row's counts come
+// from k_prep's span bucket, loaded with the chunk (one id per thread: kBucketCap ==
+// kFinThreads), so counting never waits on a dependent load; a span whose bucket
+// overflowed is counted from the whole history instead.
+constexpr int kPassDepth = 2;
+static_assert(kBucketCap == kFinThreads && kSpan == 2 * kChunk, "bucket entries per thread, chunks per span");
+
 template <int DT, bool VEC, class F>
 FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, float rep,
                       float pres, float freq, uint32_t k0, F&& f)
 {
     constexpr int EPL = DTy<DT>::EPL, SZ = DTy<DT>::SZ;
     constexpr int NL = kChunk / kFinThreads / EPL;
+    constexpr int D = kPassDepth;
     const fie_sampler_args& a = P.a;
     const int V = a.vocab, tid = threadIdx.x;
+    const int nch = (V + kChunk - 1) / kChunk;
     const char* rowp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * SZ;
     const bool mark = s != 1.0f && s >= 0x1p-30f && s <= 0x1p30f;
     const float rs = 1.0f / s;
     if (tid == 0 && k0) f(key_to_float(k0), 0u);
-    uint4 cur[NL], nxt[NL];
+    uint4 buf[D][NL];
+    uint32_t bof[D];
+    if (pen) {
+        for (int i = tid; i < P.NS; i += kFinThreads) S.snb[i] = P.w.nb[(size_t)row * P.NS + i];
+    }
+    auto issue = [&](uint4 (&b)[NL], uint32_t& of, int c) {
+        const int lo = c * kChunk;
 #pragma unroll
-    for (int j = 0; j < NL; ++j) cur[j] = load_group<DT, VEC>(rowp, (j * kFinThreads + tid) * EPL, V);
-    for (int lo = 0; lo < V; lo += kChunk) {
-        const int hi = min(lo + kChunk, V);
-        if (pen) recount(S, a, row, lo, hi);
-        if (hi < V) {
-#pragma unroll
-            for (int j = 0; j < NL; ++j) nxt[j] = load_group<DT, VEC>(rowp, hi + (j * kFinThreads + tid) * EPL, V);
+        for (int j = 0; j < NL; ++j) b[j] = load_group<DT, VEC>(rowp, lo + (j * kFinThreads + tid) * EPL, V);
+        if (pen) of = P.w.bk[((size_t)row * P.NS + lo / kSpan) * kBucketCap + tid];
+    };
+    auto count = [&](uint32_t of, int lo, int hi) {
+        for (int i = tid; i < kChunk / 4; i += kFinThreads) ((uint4*)S.cnt)[i] = make_uint4(0, 0, 0, 0);
+        __syncthreads();
+        const uint32_t nb = S.snb[lo / kSpan];
+        if (nb <= (uint32_t)kBucketCap) {
+            const uint32_t o = of - (uint32_t)(lo % kSpan);
+            if ((uint32_t)tid < nb && o < (uint32_t)kChunk) atomicAdd(&S.cnt[o], 1u);
+        } else {
+            const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
+            for (int64_t h = h0 + tid; h < h1; h += kFinThreads) {
+                const uint32_t id = (uint32_t)a.hist_ids[h];
+                if (id >= (uint32_t)lo && id < (uint32_t)hi && id != 0) atomicAdd(&S.cnt[id - lo], 1u);
+            }
         }
+        __syncthreads();
+    };
+#pragma unroll
+    for (int q = 0; q < D; ++q)
+        if (q < nch) issue(buf[q], bof[q], q);
+    for (int c = 0; c < nch; ++c) {
+        // buf[0] holds chunk c, buf[q] chunk c + q
+        const int lo = c * kChunk, hi = min(lo + kChunk, V);
+        if (pen) count(bof[0], lo, hi);
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
             const int e0 = lo + (j * kFinThreads + tid) * EPL;
@@ -242,7 +261,7 @@ FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, 
             for (int e = 0; e < EPL; ++e) {
                 const int idx = e0 + e;
                 if (idx >= V || idx == 0) continue;
-                float x = lane_get<DT>(cur[j], e);
+                float x = lane_get<DT>(buf[0][j], e);
                 if (pen) {
                     const uint32_t cc = S.cnt[idx - lo];
                     if (cc) x = penalize(x, rep, pres, freq, cc);
@@ -256,7 +275,12 @@ FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, 
         }
         if (pen) __syncthreads();
 #pragma unroll
-        for (int j = 0; j < NL; ++j) cur[j] = nxt[j];
+        for (int q = 0; q + 1 < D; ++q) {
+#pragma unroll
+            for (int j = 0; j < NL; ++j) buf[q][j] = buf[q + 1][j];
+            bof[q] = bof[q + 1];
+        }
+        if (c + D < nch) issue(buf[D - 1], bof[D - 1], c + D);
     }
     __syncthreads();
 }
@@ -603,6 +627,7 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
                 dl = dh = -1;
                 if (!gather(b, b)) return false;
             }
+            FIE_MARK(13);
             // within bin b only: composites of the lower bins (the draw's run) are larger
             uint64_t chi = ~0ull;
             if (dl >= 0) {
@@ -624,6 +649,7 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
             T = above + r.excl + r.meas;
             bc = b;
             lastc = T - above;
+            FIE_MARK(14);
         }
     }
 
@@ -664,6 +690,7 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
         if (!r.found) return false;
         tok = r.comp;
     }
+    FIE_MARK(15);
     *tk_out = tk;
     *tau_out = tau;
     *cut_out = cut;
@@ -984,13 +1011,17 @@ FIE_DEV u128 chunk_prefix(FinSmem& S, const Chunks& ch, int m)
     return r;
 }
 
-// ---------------------------------------------------------------- k_finish
-template <int DT, bool VEC>
-__global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
+// ---------------------------------------------------------------- k_finish, k_deep
+// One row's finish.  PH 0 (k_finish) settles every row its candidates can settle
+// and queues the others for PH 1 (k_deep), which runs the passes over the whole
+// row: the full-row draw, and top-L logprobs deeper than the candidates.  Both
+// phases compute the same prologue (row maximum, tile table, row mass) from the
+// partials; a queued row's DeferRec carries what PH 1 cannot recompute cheaply.
+template <int DT, bool VEC, int PH>
+FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
 {
-    __shared__ FinSmem S;
     const fie_sampler_args& a = P.a;
-    const int row = blockIdx.x, tid = threadIdx.x, NT = P.NT;
+    const int tid = threadIdx.x, NT = P.NT;
     const int32_t fl = a.flags[row];
     const bool greedy = fl & FIE_FLAG_GREEDY;
     const int lp = a.logprobs ? a.logprobs[row] : -1;
@@ -1070,6 +1101,24 @@ __global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
     u128 T = 0;
     bool deep = false;
     double lse = 0.0;
+    DeferRec dr{};
+    if (PH == 1) dr = P.w.dfr[row];
+    // PH 0: hand the row to k_deep with what is settled so far
+    auto defer = [&](uint32_t mode) {
+        if (tid == 0) {
+            DeferRec d;
+            d.tok_comp = tok_comp;
+            d.cut = cut;
+            d.tlo = (uint64_t)T;
+            d.thi = (uint64_t)(T >> 64);
+            d.token = token;
+            d.tau = tau;
+            d.mode = mode;
+            P.w.dfr[row] = d;
+            const uint32_t at = atomicAdd(&P.w.dq[0], 1u);
+            if (at < (uint32_t)a.rows) P.w.dqrows[at] = (uint32_t)row;
+        }
+    };
     if (lp >= 0) lse = log(u128_to_double(sall)) - 80.0 * 0.69314718055994530942;
 
     // Greedy rows: argmax, first index on ties (sampler.py:106,236-238).
@@ -1106,6 +1155,10 @@ __global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
         // only the complete region is ever used: candidates at or below the safety
         // key are dropped before sorting (S.cmax keeps the largest of all)
         FIE_MARK(12);
+        if (PH == 1) {
+            // the row was queued: its candidates are reloaded below only for logprobs
+            deep = dr.mode == kDeferDraw;
+        } else {
         nv = load_candidates(S, P, row, NT, n, s, k0, safe);
         cmax = S.cmax;
         FIE_MARK(13);
@@ -1135,6 +1188,14 @@ __global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
             sort_desc(S, nv);
             sorted = true;
         }
+        }
+    }
+    if (PH == 1 && dr.mode == kDeferLogprobs) {
+        token = dr.token;
+        tok_comp = dr.tok_comp;
+        tau = dr.tau;
+        cut = dr.cut;
+        T = ((u128)dr.thi << 64) | dr.tlo;
     }
 
     // Sampled rows on the sorted candidates: top-k, min-p, S, top-p cut, draw.  The
@@ -1142,7 +1203,7 @@ __global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
     // still miss it, that is not a verdict: every candidate is then loaded and
     // sorted and the selection runs again.
     FIE_MARK(4);
-    if (!greedy && !deep) {
+    if (PH == 0 && !greedy && !deep) {
         for (;;) {
             const bool partial = nv < nvall;
             bool miss = false;
@@ -1199,7 +1260,11 @@ __global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
 
     FIE_MARK(9);
     // Full-row path for sampled rows the candidates could not settle.
-    if (!greedy && deep) {
+    if (PH == 0 && !greedy && deep) {
+        defer(kDeferDraw);
+        return;
+    }
+    if (PH == 1 && !greedy && deep) {
         status |= FIE_ROW_EXACT_PATH;
         cut = 0;
         uint32_t tk = 0;
@@ -1275,6 +1340,9 @@ __global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
                     if (a.top_logprobs)
                         a.top_logprobs[o] = have ? (float)(((double)key_to_float(comp_k(c)) - (double)M) - lse) : 0.0f;
                 }
+            } else if (PH == 0) {
+                defer(kDeferLogprobs);
+                return;
             } else {
                 // the L-th largest composite over the row, the L composites >= it
                 // gathered, then sorted by one thread
@@ -1328,6 +1396,25 @@ __global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
         rr.s = s;
         P.w.res[row] = rr;
     }
+}
+
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
+{
+    __shared__ FinSmem S;
+    finish_row<DT, VEC, 0>(S, P, blockIdx.x);
+}
+
+// A fixed grid taking queued rows one at a time; every workgroup leaves once the
+// queue is drained (the count is final: k_finish has completed).
+template <int DT, bool VEC>
+__global__ __launch_bounds__(kFinThreads, 4) void k_deep(const KParams P)
+{
+    __shared__ FinSmem S;
+    const uint32_t queued = P.w.dq[0];
+    const uint32_t total = queued < (uint32_t)P.a.rows ? queued : (uint32_t)P.a.rows;
+    if (blockIdx.x >= total) return;
+    finish_row<DT, VEC, 1>(S, P, (int)P.w.dqrows[blockIdx.x]);
 }
 
 }  // namespace fie

@@ -163,7 +163,7 @@ static int fail(int code, const char* msg)
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Layout {
-    size_t maxc, sw, bound, ncand, nu, nb, bk, cand, tok0x, tok0c, bad, res, mt, ct, total;
+    size_t maxc, sw, bound, ncand, nu, nb, bk, cand, tok0x, tok0c, bad, res, mt, ct, dq, dqrows, dfr, total;
 };
 
 static bool layout_of(int32_t R, int32_t V, Layout* L)
@@ -188,6 +188,9 @@ static bool layout_of(int32_t R, int32_t V, Layout* L)
     L->res = take(r * sizeof(RowRes));
     L->mt = take(r * (NT + 1) * 4);
     L->ct = take(r * (NT + 1) * 8);
+    L->dq = take(2 * 4);
+    L->dqrows = take(r * 4);
+    L->dfr = take(r * sizeof(DeferRec));
     L->total = o;
     return true;
 }
@@ -218,6 +221,9 @@ static int ws_of(const fie_workspace* ws, int32_t rows, int32_t V, Ws* w)
     w->res = (RowRes*)(b + L.res);
     w->mt = (float*)(b + L.mt);
     w->ct = (uint64_t*)(b + L.ct);
+    w->dq = (uint32_t*)(b + L.dq);
+    w->dqrows = (uint32_t*)(b + L.dqrows);
+    w->dfr = (DeferRec*)(b + L.dfr);
     return FIE_OK;
 }
 
@@ -270,8 +276,15 @@ static int launch_scan(const KParams& P, bool vec, bool longh, hipStream_t st)
 }
 
 template <int DT>
-static int launch_finish(const KParams& P, bool vec, hipStream_t st)
+static int launch_finish(const KParams& P, bool vec, bool deep, hipStream_t st)
 {
+    if (deep) {
+        // one workgroup per queue slot; those past the queued count leave at once
+        if (vec) k_deep<DT, true><<<P.a.rows, kFinThreads, 0, st>>>(P);
+        else k_deep<DT, false><<<P.a.rows, kFinThreads, 0, st>>>(P);
+        FIE_LAUNCH_CHECK("k_deep");
+        return FIE_OK;
+    }
     if (vec) k_finish<DT, true><<<P.a.rows, kFinThreads, 0, st>>>(P);
     else k_finish<DT, false><<<P.a.rows, kFinThreads, 0, st>>>(P);
     FIE_LAUNCH_CHECK("k_finish");
@@ -297,10 +310,11 @@ static int run_stage(const KParams& P, int stage, hipStream_t st)
         default: return launch_scan<FIE_BF16>(P, vec, longh, st);
         }
     }
+    const bool deep = stage == FIE_STAGE_DEEP;
     switch (P.a.dtype) {
-    case FIE_F32: return launch_finish<FIE_F32>(P, vec, st);
-    case FIE_F16: return launch_finish<FIE_F16>(P, vec, st);
-    default: return launch_finish<FIE_BF16>(P, vec, st);
+    case FIE_F32: return launch_finish<FIE_F32>(P, vec, deep, st);
+    case FIE_F16: return launch_finish<FIE_F16>(P, vec, deep, st);
+    default: return launch_finish<FIE_BF16>(P, vec, deep, st);
     }
 }
 
@@ -365,12 +379,15 @@ int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, vo
     if (rc != FIE_OK) return rc;
     rc = run_stage(P, FIE_STAGE_SCAN, st);
     if (rc != FIE_OK) return rc;
-    return run_stage(P, FIE_STAGE_FINISH, st);
+    rc = run_stage(P, FIE_STAGE_FINISH, st);
+    if (rc != FIE_OK) return rc;
+    return run_stage(P, FIE_STAGE_DEEP, st);
 }
 
 int fie_sampler_stage(const fie_sampler_args* args, const fie_workspace* ws, int32_t stage, void* stream)
 {
-    if (stage != FIE_STAGE_PREP && stage != FIE_STAGE_SCAN && stage != FIE_STAGE_FINISH)
+    if (stage != FIE_STAGE_PREP && stage != FIE_STAGE_SCAN && stage != FIE_STAGE_FINISH &&
+        stage != FIE_STAGE_DEEP)
         return fail(FIE_E_ARG, "unknown stage");
     KParams P;
     int rc = prepare(args, ws, &P);

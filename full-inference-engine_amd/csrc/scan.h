@@ -48,6 +48,16 @@ struct RowRes {
     float s;
 };
 
+// A row k_finish hands to k_deep: what the full-row passes need beyond what k_deep
+// recomputes from the partials (mode kDeferDraw), or that the candidates settled
+// the draw and only the top-L logprobs need a pass over the row (kDeferLogprobs).
+constexpr uint32_t kDeferDraw = 1, kDeferLogprobs = 2;
+struct DeferRec {
+    uint64_t tok_comp, cut, tlo, thi;
+    int64_t token;
+    uint32_t tau, mode;
+};
+
 // Device pointers into the caller's workspace.
 struct Ws {
     uint64_t* maxc;      // [rows * NT]
@@ -64,6 +74,9 @@ struct Ws {
     RowRes* res;         // [rows]
     float* mt;           // [rows * (NT + 1)] tile maxima of y, slot 0 = token 0
     uint64_t* ct;        // [rows * (NT + 1)] tile scales C_t
+    uint32_t* dq;        // [2] rows queued for k_deep, and taken; k_scan clears both
+    uint32_t* dqrows;    // [rows] the queued rows
+    DeferRec* dfr;       // [rows]
 };
 
 struct KParams {
@@ -175,6 +188,33 @@ FIE_DEV uint32_t cand_target(int topk, int NT, bool greedy)
 template <int EPL>
 FIE_DEV int elem_index(int lo, int lane, int i) { return lo + ((i / EPL) * 64 + lane) * EPL + (i % EPL); }
 
+// (m & a) | (~m & b) in one instruction, opaque to the optimizer (a select tree
+// written in plain C++ is folded back into a runtime-indexed array in memory).
+FIE_DEV uint32_t bit_select(uint32_t m, uint32_t a, uint32_t b)
+{
+    uint32_t r;
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(m), "v"(a), "v"(b));
+    return r;
+}
+
+// x[i] for a lane-varying i < 32 as a five-level select tree: five lane masks and
+// 31 bitfield selects, where a plain runtime index into registers becomes a
+// 31-step compare and select chain.
+FIE_DEV float pick32(const float (&x)[32], uint32_t i)
+{
+    uint32_t v[16];
+    const uint32_t m0 = 0u - (i & 1u);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = bit_select(m0, __float_as_uint(x[2 * k + 1]), __float_as_uint(x[2 * k]));
+#pragma unroll
+    for (int lvl = 1; lvl < 5; ++lvl) {
+        const uint32_t m = 0u - ((i >> lvl) & 1u);
+#pragma unroll
+        for (int k = 0; k < (16 >> lvl); ++k) v[k] = bit_select(m, v[2 * k + 1], v[2 * k]);
+    }
+    return __uint_as_float(v[0]);
+}
+
 // Largest t (refining `pre` over bits hi..lo) with at least `target` of the keys
 // k[0..N) of the wave's lanes at or above t: a radix select by ballot counts.
 template <int N>
@@ -278,6 +318,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
     const float s = greedy ? 1.0f : a.scale[row];       // greedy rows stay unscaled (sampler.py:182)
     const char* rowp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * SZ;
     const size_t slot = (size_t)row * NT + tile;
+    if (blockIdx.x == 0 && blockIdx.y == 0 && tid < 2) P.w.dq[tid] = 0u;   // k_deep's queue, filled by k_finish
 
     // 1. The span's history bucket (k_prep), then every load of the tile: the
     //    history is counted while the logits are in flight.
@@ -498,6 +539,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
         const int valid = V - lo < kTile ? V - lo : kTile;
         const uint32_t half = (uint32_t)((valid + EPL - 1) / EPL / 2);
         if (c > half) c = half > 8u ? half : 8u;
+        c = __builtin_amdgcn_readfirstlane(c);               // uniform in the wave
         uint32_t gk[NG];
 #pragma unroll
         for (int g = 0; g < NG; ++g) gk[g] = gm[g] == gm[g] ? fkey(gm[g] + 0.0f) : 0u;
@@ -508,19 +550,22 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
         // stage: per lane, its tokens at or above the floor, by a float compare
         // against the floor's value (NaN fails it); a floor whose value is not a
         // number (a key of the NaN range) or 0 (all tokens) compares by key instead
-        const float fv = key_to_float(floor_key);
-        const bool fv_ok = floor_key > kKeyNegInf && floor_key <= kKeyPosInf;
-        uint32_t mask = 0;
+        // (the floor is wave-uniform: one branch for the wave, straight-line compares)
+        const uint32_t fk = __builtin_amdgcn_readfirstlane(floor_key);
+        const float fv = key_to_float(fk);
+        uint32_t mask = 0, pmask = 0;      // tokens and slots at or above the floor
+        if (fk > kKeyNegInf && fk <= kKeyPosInf) {
 #pragma unroll
-        for (int i = 0; i < kEPT; ++i) {
-            const bool ge = fv_ok ? (x[i] >= fv) : (x[i] == x[i] && fkey(x[i] + 0.0f) >= floor_key);
-            mask |= ge ? (1u << i) : 0u;
-        }
-        uint32_t pmask = 0;      // slots at or above the floor
+            for (int i = 0; i < kEPT; ++i) mask |= (x[i] >= fv) ? (1u << i) : 0u;
 #pragma unroll
-        for (int q = 0; q < kPS; ++q) {
-            const bool ge = fv_ok ? (pv[q] >= fv) : (pv[q] == pv[q] && fkey(pv[q] + 0.0f) >= floor_key);
-            pmask |= ge ? (1u << q) : 0u;
+            for (int q = 0; q < kPS; ++q) pmask |= (pv[q] >= fv) ? (1u << q) : 0u;
+        } else {
+#pragma unroll
+            for (int i = 0; i < kEPT; ++i)
+                mask |= ((x[i] == x[i]) & (fkey(x[i] + 0.0f) >= fk)) ? (1u << i) : 0u;
+#pragma unroll
+            for (int q = 0; q < kPS; ++q)
+                pmask |= ((pv[q] == pv[q]) & (fkey(pv[q] + 0.0f) >= fk)) ? (1u << q) : 0u;
         }
         uint32_t E;
         uint32_t at = dwave_excl_scan_u32((uint32_t)(__builtin_popcount(mask) + __builtin_popcount(pmask)), &E);
@@ -528,7 +573,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
         for (uint32_t b = mask; b; b &= b - 1) {
             const int i = __builtin_ctz(b);
             if (at < (uint32_t)kStageW)
-                st[at] = comp_key(fkey(x[i] + 0.0f), (uint32_t)elem_index<EPL>(lo, lane, i));
+                st[at] = comp_key(fkey(pick32(x, (uint32_t)i) + 0.0f), (uint32_t)elem_index<EPL>(lo, lane, i));
             ++at;
         }
         if (__ballot(pmask != 0) != 0) {
@@ -544,7 +589,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
         // at most `cap` emitted per tile (ties at the c-th key beyond it stay
         // below the bound)
         const uint32_t cap = (uint32_t)kCapW;
-        uint32_t bound = floor_key ? floor_key : 1u;
+        uint32_t bound = fk ? fk : 1u;
         if (E > (uint32_t)kStageW) {
             // more than kStageW tokens in the floor's bin (massive ties): emit
             // nothing and mark the tile incomplete; the row takes the full-row path

@@ -18,7 +18,7 @@ FIE_F32, FIE_F16, FIE_BF16 = 0, 1, 2
 FIE_FLAG_GREEDY, FIE_FLAG_PENALTY = 1, 2
 FIE_ROW_EXACT_PATH = 1
 FIE_ROW_UNCOUNTED_IDS = 2
-FIE_STAGE_PREP, FIE_STAGE_SCAN, FIE_STAGE_FINISH = 0, 1, 2
+FIE_STAGE_PREP, FIE_STAGE_SCAN, FIE_STAGE_FINISH, FIE_STAGE_DEEP = 0, 1, 2, 3
 LP_COLS = 20
 TILE = 8192
 MAX_VOCAB = 64 * TILE

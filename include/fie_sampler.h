@@ -136,8 +136,9 @@ typedef struct fie_workspace {
    most `vocab` (0 on invalid sizes). */
 size_t fie_sampler_workspace_size(int32_t max_rows, int32_t vocab);
 
-/* One sampler step: sampler.py:81-117 minus host bookkeeping.  Two kernels: one
-   streaming read of the logits, then one workgroup per row. */
+/* One sampler step: sampler.py:81-117 minus host bookkeeping.  Four kernels: the
+   penalty histories bucketed by span, one streaming read of the logits, one
+   workgroup per row, then the rows the candidates could not settle. */
 int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, void* stream);
 
 /* The kernels of fie_sampler_sample, one at a time, in this order (same args and
@@ -146,7 +147,8 @@ int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, vo
 enum {
     FIE_STAGE_PREP = 0,        /* the penalty histories bucketed by span (no-op without penalties) */
     FIE_STAGE_SCAN = 1,        /* the streaming pass over the logits */
-    FIE_STAGE_FINISH = 2,      /* the per-row selection and draw */
+    FIE_STAGE_FINISH = 2,      /* the per-row selection and draw from the candidates */
+    FIE_STAGE_DEEP = 3,        /* the rows FINISH queued: passes over the whole row (no-op when none) */
 };
 int fie_sampler_stage(const fie_sampler_args* args, const fie_workspace* ws, int32_t stage,
                       void* stream);
