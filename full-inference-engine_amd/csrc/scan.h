@@ -359,6 +359,10 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
                 atomicAdd(&L.uniq[o / kTile], 1u);
             }
         };
+#ifdef FIE_X_NOCOUNT
+        if (nb <= (uint32_t)kBucketCap) {
+        } else
+#endif
         if (nb <= (uint32_t)kBucketCap) {
             if ((uint32_t)tid < nb) count(e0);
             for (uint32_t i = tid + kScanThreads; i < nb; i += kScanThreads) count(P.w.bk[rs * kBucketCap + i]);
@@ -414,10 +418,12 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
             }
         } else if (__ballot(mine != 0) != 0) {
             // a set bit ORs a quiet NaN's exponent and quiet bit into the value
+#ifndef FIE_X_NOMARK
 #pragma unroll
             for (int i = 0; i < kEPT; ++i)
                 x[i] = __int_as_float(__float_as_int(x[i]) |
                                       (__builtin_amdgcn_sbfe((int)mine, (unsigned)i, 1u) & 0x7FC00000));
+#endif
             uint32_t b = mine;
 #pragma unroll
             for (int q = 0; q < kPS; ++q) {
@@ -428,7 +434,11 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
             }
 #pragma unroll
             for (int q = 0; q < kPS; ++q)
+#ifndef FIE_X_NOLOAD
                 if (pidx[q] != 0xFFFFFFFFu) pv[q] = load_elem<DT>(rowp, pidx[q]);
+#else
+                if (pidx[q] != 0xFFFFFFFFu) pv[q] = 1.0f;
+#endif
 #pragma unroll
             for (int q = 0; q < kPS; ++q)
                 if (pidx[q] != 0xFFFFFFFFu) pv[q] = penalize(pv[q], rep, pres, freq, count_of((int)pidx[q] - slo));
@@ -462,6 +472,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
     float m = gm[0];
 #pragma unroll
     for (int g = 1; g < NG; ++g) m = __builtin_fmaxf(m, gm[g]);
+    const float mx = m;      // the lane's maximum over its own tokens (slots aside)
 #pragma unroll
     for (int q = 0; q < kPS; ++q) m = __builtin_fmaxf(m, pv[q]);
     const uint32_t lkey = m == m ? fkey(m + 0.0f) : 0u;
@@ -528,8 +539,8 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
         if (lane == 0) P.w.sw[slot] = tot;
     }
 
-    // 6. The tile's top tokens.  The floor is the largest 12- or 20-bit key prefix with
-    //    at least c group maxima at or above it, so at least c tokens are; tokens
+    // 6. The tile's top tokens.  The floor is the largest 20-bit key prefix with at
+    //    least c lane or group maxima at or above it, so at least c tokens are; tokens
     //    at or above it are staged in LDS, and when more than kCapW are, the c-th
     //    largest staged key is found by a full-width ballot select.
     if (need_cand) {
@@ -540,13 +551,19 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
         const uint32_t half = (uint32_t)((valid + EPL - 1) / EPL / 2);
         if (c > half) c = half > 8u ? half : 8u;
         c = __builtin_amdgcn_readfirstlane(c);               // uniform in the wave
-        uint32_t gk[NG];
+        // Small c: a 20-bit prefix over the 64 lane maxima (c lanes hold a token at
+        // or above it; one ballot per bit).  Wide rows: a 20-bit prefix over the 256
+        // group maxima, which keeps the tokens at or above it within staging.
+        uint32_t floor_key;
+        if (c > (uint32_t)kCandMin) {
+            uint32_t gk[NG];
 #pragma unroll
-        for (int g = 0; g < NG; ++g) gk[g] = gm[g] == gm[g] ? fkey(gm[g] + 0.0f) : 0u;
-        // a 12-bit prefix for small c; a 20-bit one for wide rows, whose floor
-        // bucket would otherwise hold more group maxima than staging can take
-        const uint32_t floor_key = c > (uint32_t)kCandMin ? ballot_select(gk, c, 0u, 31, 12)
-                                                          : ballot_select(gk, c, 0u, 31, 20);
+            for (int g = 0; g < NG; ++g) gk[g] = gm[g] == gm[g] ? fkey(gm[g] + 0.0f) : 0u;
+            floor_key = ballot_select(gk, c, 0u, 31, 12);
+        } else {
+            const uint32_t lk[1] = {mx == mx ? fkey(mx + 0.0f) : 0u};
+            floor_key = ballot_select(lk, c, 0u, 31, 12);
+        }
         // stage: per lane, its tokens at or above the floor, by a float compare
         // against the floor's value (NaN fails it); a floor whose value is not a
         // number (a key of the NaN range) or 0 (all tokens) compares by key instead
