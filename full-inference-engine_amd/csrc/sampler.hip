@@ -16,6 +16,7 @@
 #include <mutex>
 
 #include "finish.h"
+#include "lmhead.h"
 #include "fie_sampler.h"
 
 namespace fie {
@@ -318,6 +319,25 @@ static int run_stage(const KParams& P, int stage, hipStream_t st)
     }
 }
 
+template <int DT>
+static int launch_lmhead(const KParams& P, const void* hidden, const void* weight, int H, bool vec, bool longh,
+                         hipStream_t st)
+{
+    const int nrb = (P.a.rows + kLhRows - 1) / kLhRows;
+    const int grid = 8 * ((P.NT + 7) / 8) * nrb;
+    const uint16_t* h = (const uint16_t*)hidden;
+    const uint16_t* w = (const uint16_t*)weight;
+    if (vec) {
+        if (longh) k_lmhead<DT, true, true><<<grid, kLhThreads, 0, st>>>(P, h, w, H, nrb);
+        else k_lmhead<DT, true, false><<<grid, kLhThreads, 0, st>>>(P, h, w, H, nrb);
+    } else {
+        if (longh) k_lmhead<DT, false, true><<<grid, kLhThreads, 0, st>>>(P, h, w, H, nrb);
+        else k_lmhead<DT, false, false><<<grid, kLhThreads, 0, st>>>(P, h, w, H, nrb);
+    }
+    FIE_LAUNCH_CHECK("k_lmhead");
+    return FIE_OK;
+}
+
 static int prepare(const fie_sampler_args* args, const fie_workspace* ws, KParams* P)
 {
     int rc = check_args(args);
@@ -378,6 +398,33 @@ int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, vo
     rc = run_stage(P, FIE_STAGE_PREP, st);
     if (rc != FIE_OK) return rc;
     rc = run_stage(P, FIE_STAGE_SCAN, st);
+    if (rc != FIE_OK) return rc;
+    rc = run_stage(P, FIE_STAGE_FINISH, st);
+    if (rc != FIE_OK) return rc;
+    return run_stage(P, FIE_STAGE_DEEP, st);
+}
+
+int fie_sampler_lmhead_sample(const fie_sampler_args* args, const void* hidden, const void* weight,
+                              int32_t hidden_dim, const fie_workspace* ws, void* stream)
+{
+    if (!args) return fail(FIE_E_ARG, "args is NULL");
+    if (args->dtype != FIE_F16 && args->dtype != FIE_BF16)
+        return fail(FIE_E_ARG, "the fused lm_head takes fp16 or bf16 (the logits dtype is the model's)");
+    if (hidden_dim < kLhKAlign || hidden_dim % kLhKAlign != 0)
+        return fail(FIE_E_ARG, "hidden_dim must be a positive multiple of 128");
+    KParams P;
+    int rc = prepare(args, ws, &P);
+    if (rc != FIE_OK || args->rows == 0) return rc;
+    if (!hidden || !weight) return fail(FIE_E_ARG, "hidden or weight is NULL");
+    if (((uintptr_t)hidden % 16) != 0 || ((uintptr_t)weight % 16) != 0)
+        return fail(FIE_E_ARG, "hidden and weight must be 16-byte aligned");
+    hipStream_t st = (hipStream_t)stream;
+    rc = run_stage(P, FIE_STAGE_PREP, st);
+    if (rc != FIE_OK) return rc;
+    const bool vec = vec_ok(args->logits, args->row_stride, 2);
+    const bool longh = args->apply_penalties && args->max_row_hist > 65535;
+    rc = args->dtype == FIE_F16 ? launch_lmhead<FIE_F16>(P, hidden, weight, hidden_dim, vec, longh, st)
+                                : launch_lmhead<FIE_BF16>(P, hidden, weight, hidden_dim, vec, longh, st);
     if (rc != FIE_OK) return rc;
     rc = run_stage(P, FIE_STAGE_FINISH, st);
     if (rc != FIE_OK) return rc;

@@ -291,94 +291,56 @@ __global__ __launch_bounds__(kPrepThreads) void k_prep(const KParams P)
     }
 }
 
-// ---------------------------------------------------------------- k_scan
-template <int DT, bool VEC, bool LONGH>
-__global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
+// Per-row settings the tile pass reads (sampler.py:182 leaves greedy rows unscaled).
+struct RowCfg {
+    bool greedy, pen, need_mass, need_cand;
+    int lp, topk;
+    float s, rep, pres, freq;
+};
+
+FIE_DEV RowCfg row_cfg(const fie_sampler_args& a, int row)
 {
-    constexpr int EPL = DTy<DT>::EPL, SZ = DTy<DT>::SZ, NL = kEPT / EPL;
-    constexpr int CW = LONGH ? kSpan : kSpan / 2;
-    __shared__ ScanSmem<LONGH> L;
-
-    const fie_sampler_args& a = P.a;
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int row = blockIdx.y;
-    const int NT = P.NT, V = a.vocab;
-    const int slo = blockIdx.x * kSpan;                 // first token of the span
-    const int shi = min(slo + kSpan, V);
-    const int tile = blockIdx.x * kWavesPerWG + wv;     // this wave's tile
-    const int lo = tile * kTile;
-    const bool live = tile < NT;                        // waves past the row's end idle
+    RowCfg c;
     const int32_t fl = a.flags[row];
-    const bool greedy = fl & FIE_FLAG_GREEDY;
-    const int lp = a.logprobs ? a.logprobs[row] : -1;
-    const bool pen = a.apply_penalties && (fl & FIE_FLAG_PENALTY);
-    const int topk = greedy ? 0 : a.top_k[row];
-    const bool need_mass = lp >= 0 || (!greedy && topk == 0);
-    const bool need_cand = !greedy || lp > 0;
-    const float s = greedy ? 1.0f : a.scale[row];       // greedy rows stay unscaled (sampler.py:182)
-    const char* rowp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * SZ;
+    c.greedy = fl & FIE_FLAG_GREEDY;
+    c.lp = a.logprobs ? a.logprobs[row] : -1;
+    c.pen = a.apply_penalties && (fl & FIE_FLAG_PENALTY);
+    c.topk = c.greedy ? 0 : a.top_k[row];
+    c.need_mass = c.lp >= 0 || (!c.greedy && c.topk == 0);
+    c.need_cand = !c.greedy || c.lp > 0;
+    c.s = c.greedy ? 1.0f : a.scale[row];
+    c.rep = 1.0f;
+    c.pres = 0.0f;
+    c.freq = 0.0f;
+    if (c.pen) {
+        c.rep = a.repetition[row];
+        c.pres = a.presence[row];
+        c.freq = a.frequency[row];
+    }
+    return c;
+}
+
+// One wave's pass over one 2048-token tile of one row, its tokens already in
+// registers (raw, the lane layout of load_group): penalties, the tile maximum,
+// the tile mass and the candidates, written to the tile's partials.  `rowp` is
+// the row's token 0 for the re-read of penalised tokens (global memory, or a
+// producer's staging copy); pbits/cnt hold the penalty marks and counts of tokens
+// pbase.. (u16 halves, u32 words when LONGH); `stage` is kStageW words of the
+// wave's own LDS.
+template <int DT, bool LONGH>
+FIE_DEV void scan_tile(const KParams& P, const RowCfg& rc, int row, int tile,
+                       uint4 (&raw)[kEPT / DTy<DT>::EPL], const char* rowp,
+                       const uint32_t* pbits, const uint32_t* cnt, int pbase, uint64_t* stage)
+{
+    constexpr int EPL = DTy<DT>::EPL, NL = kEPT / EPL;
+    const fie_sampler_args& a = P.a;
+    const int lane = threadIdx.x & 63;
+    const int NT = P.NT, V = a.vocab;
+    const int lo = tile * kTile;
     const size_t slot = (size_t)row * NT + tile;
-    if (blockIdx.x == 0 && blockIdx.y == 0 && tid < 2) P.w.dq[tid] = 0u;   // k_deep's queue, filled by k_finish
-
-    // 1. The span's history bucket (k_prep), then every load of the tile: the
-    //    history is counted while the logits are in flight.
-    const size_t rs = (size_t)row * P.NS + blockIdx.x;
-    uint32_t nb = 0, e0 = 0;
-    if (pen) {
-        nb = P.w.nb[rs];
-        e0 = P.w.bk[rs * kBucketCap + tid];
-    }
-    uint4 raw[NL];
-#pragma unroll
-    for (int j = 0; j < NL; ++j)
-        raw[j] = live ? load_group<DT, VEC>(rowp, lo + (j * 64 + lane) * EPL, V) : make_uint4(0, 0, 0, 0);
-
-    // 2. Penalty counts of the span's ids (sampler.py:134-144), shared by the four
-    //    waves.  A token's first count sets its bit in pbits and counts it as a
-    //    distinct id of its tile.  A bucket that overflowed (more than kBucketCap
-    //    ids in the span) is replaced by a scan of the row's whole history.
-    float rep = 1.0f, pres = 0.0f, freq = 0.0f;
-    if (pen) {
-        rep = a.repetition[row];
-        pres = a.presence[row];
-        freq = a.frequency[row];
-        for (int i = tid; i < CW / 4; i += kScanThreads) ((uint4*)L.cnt)[i] = make_uint4(0, 0, 0, 0);
-        for (int i = tid; i < kSpan / 32; i += kScanThreads) L.pbits[i] = 0;
-        if (tid < kWavesPerWG) L.uniq[tid] = 0;
-        __syncthreads();
-        auto count = [&](uint32_t o) {
-            uint32_t was;
-            if (LONGH) {
-                was = atomicAdd(&L.cnt[o], 1u);
-            } else {
-                const uint32_t sh = (o & 1) * 16;
-                was = (atomicAdd(&L.cnt[o >> 1], 1u << sh) >> sh) & 0xFFFFu;
-            }
-            if (was == 0) {
-                atomicOr(&L.pbits[o >> 5], 1u << (o & 31));
-                atomicAdd(&L.uniq[o / kTile], 1u);
-            }
-        };
-#ifdef FIE_X_NOCOUNT
-        if (nb <= (uint32_t)kBucketCap) {
-        } else
-#endif
-        if (nb <= (uint32_t)kBucketCap) {
-            if ((uint32_t)tid < nb) count(e0);
-            for (uint32_t i = tid + kScanThreads; i < nb; i += kScanThreads) count(P.w.bk[rs * kBucketCap + i]);
-        } else {
-            const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
-            for (int64_t h = h0 + tid; h < h1; h += kScanThreads) {
-                const uint32_t id = (uint32_t)a.hist_ids[h];
-                if (id != 0 && id >= (uint32_t)slo && id < (uint32_t)shi) count(id - (uint32_t)slo);
-            }
-        }
-        __syncthreads();
-        if (live && lane == 0) P.w.nu[slot] = L.uniq[wv];
-    } else {
-        if (live && lane == 0) P.w.nu[slot] = 0;
-    }
-    if (!live) return;
+    const bool greedy = rc.greedy, pen = rc.pen, need_mass = rc.need_mass, need_cand = rc.need_cand;
+    const int topk = rc.topk;
+    const float s = rc.s, rep = rc.rep, pres = rc.pres, freq = rc.freq;
 
     // 3. The penalised logits (sampler.py:169-175).  Registers are indexed only
     //    statically (a runtime index into x[] turns into a select per element):
@@ -401,16 +363,16 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
         uint32_t mine = 0;   // bit i: the lane's token i is penalised
 #pragma unroll
         for (int j = 0; j < NL; ++j) {
-            const int o = lo - slo + (j * 64 + lane) * EPL;
-            mine |= ((L.pbits[o >> 5] >> (o & 31)) & ((1u << EPL) - 1)) << (j * EPL);
+            const int o = lo - pbase + (j * 64 + lane) * EPL;
+            mine |= ((pbits[o >> 5] >> (o & 31)) & ((1u << EPL) - 1)) << (j * EPL);
         }
         auto count_of = [&](int o) -> uint32_t {
-            return LONGH ? L.cnt[o] : ((L.cnt[o >> 1] >> ((o & 1) * 16)) & 0xFFFFu);
+            return LONGH ? cnt[o] : ((cnt[o >> 1] >> ((o & 1) * 16)) & 0xFFFFu);
         };
         if (__ballot(__builtin_popcount(mine) > kPS) != 0) {
             for (uint32_t b = mine; b; b &= b - 1) {
                 const int i = __builtin_ctz(b);
-                const int o = lo - slo + ((i / EPL) * 64 + lane) * EPL + (i % EPL);
+                const int o = lo - pbase + ((i / EPL) * 64 + lane) * EPL + (i % EPL);
                 x[i] = penalize(x[i], rep, pres, freq, count_of(o));
                 // a finite, nonzero value outside Markstein's range (extreme penalty
                 // parameters) sends the wave's fp16 mass loop to the checked divide
@@ -441,7 +403,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
 #endif
 #pragma unroll
             for (int q = 0; q < kPS; ++q)
-                if (pidx[q] != 0xFFFFFFFFu) pv[q] = penalize(pv[q], rep, pres, freq, count_of((int)pidx[q] - slo));
+                if (pidx[q] != 0xFFFFFFFFu) pv[q] = penalize(pv[q], rep, pres, freq, count_of((int)pidx[q] - pbase));
         }
     }
     // Tokens outside the tile read NaN from here on: token 0 (a tile of its own,
@@ -586,7 +548,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
         }
         uint32_t E;
         uint32_t at = dwave_excl_scan_u32((uint32_t)(__builtin_popcount(mask) + __builtin_popcount(pmask)), &E);
-        uint64_t* st = L.stage[wv];
+        uint64_t* st = stage;
         for (uint32_t b = mask; b; b &= b - 1) {
             const int i = __builtin_ctz(b);
             if (at < (uint32_t)kStageW)
@@ -650,6 +612,88 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
             P.w.bound[slot] = over ? 0xFFFFFFFFu : bound;
         }
     }
+}
+
+// ---------------------------------------------------------------- k_scan
+template <int DT, bool VEC, bool LONGH>
+__global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
+{
+    constexpr int EPL = DTy<DT>::EPL, SZ = DTy<DT>::SZ, NL = kEPT / EPL;
+    constexpr int CW = LONGH ? kSpan : kSpan / 2;
+    __shared__ ScanSmem<LONGH> L;
+
+    const fie_sampler_args& a = P.a;
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int row = blockIdx.y;
+    const int NT = P.NT, V = a.vocab;
+    const int slo = blockIdx.x * kSpan;                 // first token of the span
+    const int shi = min(slo + kSpan, V);
+    const int tile = blockIdx.x * kWavesPerWG + wv;     // this wave's tile
+    const int lo = tile * kTile;
+    const bool live = tile < NT;                        // waves past the row's end idle
+    const RowCfg rc = row_cfg(a, row);
+    const bool pen = rc.pen;
+    const char* rowp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * SZ;
+    const size_t slot = (size_t)row * NT + tile;
+    if (blockIdx.x == 0 && blockIdx.y == 0 && tid < 2) P.w.dq[tid] = 0u;   // k_deep's queue, filled by k_finish
+
+    // 1. The span's history bucket (k_prep), then every load of the tile: the
+    //    history is counted while the logits are in flight.
+    const size_t rs = (size_t)row * P.NS + blockIdx.x;
+    uint32_t nb = 0, e0 = 0;
+    if (pen) {
+        nb = P.w.nb[rs];
+        e0 = P.w.bk[rs * kBucketCap + tid];
+    }
+    uint4 raw[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j)
+        raw[j] = live ? load_group<DT, VEC>(rowp, lo + (j * 64 + lane) * EPL, V) : make_uint4(0, 0, 0, 0);
+
+    // 2. Penalty counts of the span's ids (sampler.py:134-144), shared by the four
+    //    waves.  A token's first count sets its bit in pbits and counts it as a
+    //    distinct id of its tile.  A bucket that overflowed (more than kBucketCap
+    //    ids in the span) is replaced by a scan of the row's whole history.
+    if (pen) {
+        for (int i = tid; i < CW / 4; i += kScanThreads) ((uint4*)L.cnt)[i] = make_uint4(0, 0, 0, 0);
+        for (int i = tid; i < kSpan / 32; i += kScanThreads) L.pbits[i] = 0;
+        if (tid < kWavesPerWG) L.uniq[tid] = 0;
+        __syncthreads();
+        auto count = [&](uint32_t o) {
+            uint32_t was;
+            if (LONGH) {
+                was = atomicAdd(&L.cnt[o], 1u);
+            } else {
+                const uint32_t sh = (o & 1) * 16;
+                was = (atomicAdd(&L.cnt[o >> 1], 1u << sh) >> sh) & 0xFFFFu;
+            }
+            if (was == 0) {
+                atomicOr(&L.pbits[o >> 5], 1u << (o & 31));
+                atomicAdd(&L.uniq[o / kTile], 1u);
+            }
+        };
+#ifdef FIE_X_NOCOUNT
+        if (nb <= (uint32_t)kBucketCap) {
+        } else
+#endif
+        if (nb <= (uint32_t)kBucketCap) {
+            if ((uint32_t)tid < nb) count(e0);
+            for (uint32_t i = tid + kScanThreads; i < nb; i += kScanThreads) count(P.w.bk[rs * kBucketCap + i]);
+        } else {
+            const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
+            for (int64_t h = h0 + tid; h < h1; h += kScanThreads) {
+                const uint32_t id = (uint32_t)a.hist_ids[h];
+                if (id != 0 && id >= (uint32_t)slo && id < (uint32_t)shi) count(id - (uint32_t)slo);
+            }
+        }
+        __syncthreads();
+        if (live && lane == 0) P.w.nu[slot] = L.uniq[wv];
+    } else {
+        if (live && lane == 0) P.w.nu[slot] = 0;
+    }
+    if (!live) return;
+
+    scan_tile<DT, LONGH>(P, rc, row, tile, raw, rowp, L.pbits, L.cnt, slo, L.stage[wv]);
 }
 
 }  // namespace fie

@@ -294,6 +294,46 @@ class FusedSampler:
                                                  self._stream_ptr()), "fie_sampler_uniforms")
         return out
 
+    def launch_lmhead(self, args: SamplerArgs, hidden: torch.Tensor, weight: torch.Tensor) -> None:
+        """The fused lm_head step: args.logits receives hidden @ weight.T and the
+        sampler runs on it (fie_sampler_lmhead_sample)."""
+        ws = self.ensure_workspace(args.rows, args.vocab)
+        rc = self.lib.fie_sampler_lmhead_sample(ctypes.byref(args), hidden.data_ptr(), weight.data_ptr(),
+                                                hidden.shape[1], ctypes.byref(ws), self._stream_ptr())
+        _lib.check(rc, "fie_sampler_lmhead_sample")
+
+    def lmhead_step(self, hidden: torch.Tensor, weight: torch.Tensor, hp: HostParams,
+                    logits: torch.Tensor | None = None):
+        """One step from the last hidden states: logits = hidden @ weight.T (the model's
+        output layer, continuous_batching.py:1345) fused with the sampler.  hidden
+        [rows, H] and weight [vocab, H] share one dtype, fp16 or bf16, which the logits
+        take too.  Returns (outputs, args, buffers, logits) after one sync."""
+        if hidden.dtype not in (torch.float16, torch.bfloat16) or weight.dtype != hidden.dtype:
+            raise ValueError("hidden and weight must share one dtype, float16 or bfloat16")
+        if hidden.dim() != 2 or weight.dim() != 2 or hidden.shape[1] != weight.shape[1]:
+            raise ValueError("hidden [rows, H] and weight [vocab, H] must agree on H")
+        hidden, weight = hidden.contiguous(), weight.contiguous()
+        rows, vocab = hidden.shape[0], weight.shape[0]
+        if logits is None:
+            logits = torch.empty((rows, vocab), dtype=hidden.dtype, device=self.device)
+        elif (logits.dtype != hidden.dtype or tuple(logits.shape) != (rows, vocab)
+              or logits.stride(1) != 1 or logits.stride(0) < vocab):
+            raise ValueError("logits must be a [rows, vocab] buffer of the model dtype with unit column stride")
+        buf = self.step_buffers(rows, hp.tail_ints())
+        buf.stage(hp)
+        stream = torch.cuda.current_stream(self.device)
+        buf.upload(stream)
+        if hp.hist_ends is not None and hp.hist_write_dst.shape[0]:
+            n = int(hp.hist_write_dst.shape[0])
+            o = buf.ptr("hist_ids")
+            _lib.check(self.lib.fie_sampler_history_write(hp.hist_store.ids.data_ptr(), o, o + 8 * n, n,
+                                                          self._stream_ptr()), "fie_sampler_history_write")
+        args = self.build_args(logits, buf, hp)
+        self.launch_lmhead(args, hidden, weight)
+        buf.download(stream)
+        stream.synchronize()
+        return buf.outputs(), args, buf, logits
+
     # ------------------------------------------------------------------ a full step
     def step(self, logits: torch.Tensor, hp: HostParams):
         """Upload, launch, download; returns (outputs, args, buffers) after one sync."""

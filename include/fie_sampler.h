@@ -141,6 +141,20 @@ size_t fie_sampler_workspace_size(int32_t max_rows, int32_t vocab);
    workgroup per row, then the rows the candidates could not settle. */
 int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, void* stream);
 
+/* fie_sampler_sample with the model's output projection fused in front of it.  The
+   reference computes the logits as `self._lm_head()(hidden)`, an nn.Linear without bias
+   in the model dtype (continuous_batching.py:1345,1594,2225), and passes that buffer to
+   the sampler (:1926-1928).  Here one kernel computes args->logits = hidden · weightᵀ
+   (fp32 accumulation, rounded to nearest even in args->dtype, which must be FIE_F16 or
+   FIE_BF16, the dtype of hidden and weight) and, from the values it wrote, the
+   per-tile partials the sampler's streaming pass would read back; the rest of the
+   chain is fie_sampler_sample's.  args->logits is written (row stride args->row_stride)
+   and must hold rows x vocab.  hidden: [rows, hidden_dim] row-major; weight:
+   [vocab, hidden_dim] row-major (nn.Linear's layout); both 16-byte aligned, and
+   hidden_dim a multiple of 128. */
+int fie_sampler_lmhead_sample(const fie_sampler_args* args, const void* hidden, const void* weight,
+                              int32_t hidden_dim, const fie_workspace* ws, void* stream);
+
 /* The kernels of fie_sampler_sample, one at a time, in this order (same args and
    workspace each time).  No counterpart in the reference: it exists so a profiler
    or a benchmark can time each kernel of the chain separately. */

@@ -409,3 +409,50 @@ def test_cexp_matches_oracle(fs):
     got = fs.cexp(d.to(DEV)).cpu().numpy()
     want = O.cexp(d.numpy()[::97])
     np.testing.assert_array_equal(got[::97].view(np.uint32), want.view(np.uint32))
+
+
+# ---------------------------------------------------------------- fused lm_head (f3)
+def _lmhead_case(rows, vocab, H, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    hidden = torch.randn(rows, H, generator=g).to(dtype)
+    weight = (torch.randn(vocab, H, generator=g) * (2.5 / H ** 0.5)).to(dtype)
+    rng = np.random.default_rng(seed)
+    params = _mixed_params(rows, vocab, rng)
+    ctx = [list(rng.integers(0, vocab + 3, size=int(rng.integers(0, 300)))) + ([0] if r % 2 else [])
+           for r in range(rows)]
+    return hidden, weight, params, ctx, rng.random(rows)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,vocab,H", [(5, 5000, 128), (70, 20001, 512), (130, 151936, 1024)])
+def test_lmhead_fused_matches_the_two_step_path(fs, dtype, rows, vocab, H):
+    """fie_sampler_lmhead_sample: its logits are hidden @ weight.T to within one
+    rounding of the model dtype (the fp32 sum's order differs from a library GEMM's),
+    and every sampler output equals fie_sampler_sample's on those same logits, bit
+    for bit: the fused epilogue computes the partials k_scan would have."""
+    hidden, weight, params, ctx, u = _lmhead_case(rows, vocab, H, dtype, rows * 31 + H)
+    hp = resolve_params(params, vocab, u, ctx)
+    out, _, _, logits = fs.lmhead_step(hidden.to(DEV), weight.to(DEV), hp)
+    ref = hidden.to(DEV).float() @ weight.to(DEV).float().T
+    # the fused value is the fp32 reference rounded to the dtype, or a neighbour of it
+    # (one ulp: the two fp32 sums may round to either side of a midpoint)
+    got = logits.view(torch.int16).int()
+    want = ref.to(dtype).view(torch.int16).int()
+    # or, where the sum cancels, within the fp32 accumulation error of either order
+    mag = hidden.to(DEV).float().abs() @ weight.to(DEV).float().abs().T
+    near = ((got - want).abs() <= 1) | ((logits.float() - ref).abs() <= 32 * 2.0 ** -24 * mag)
+    assert bool(near.all()), int((~near).sum())
+    two, _, _ = fs.step(logits, hp)
+    for name in ("tokens", "status", "tk_key", "cut_comp", "row_max", "kept_mass", "row_mass",
+                 "chosen_lp", "top_ids", "top_lp"):
+        np.testing.assert_array_equal(out[name], two[name], err_msg=name)
+
+
+def test_lmhead_rejects_what_it_cannot_run(fs):
+    hidden = torch.zeros(4, 100, dtype=torch.bfloat16, device=DEV)
+    weight = torch.zeros(300, 100, dtype=torch.bfloat16, device=DEV)
+    hp = resolve_params([SamplingParams()] * 4, 300, np.zeros(4), None)
+    with pytest.raises(RuntimeError, match="multiple of 128"):
+        fs.lmhead_step(hidden, weight, hp)
+    with pytest.raises(ValueError):
+        fs.lmhead_step(hidden.float(), weight.float(), hp)

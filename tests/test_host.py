@@ -330,6 +330,20 @@ def test_sample_rejects_bad_workspaces():
     assert lib.fie_sampler_stage(ctypes.byref(a), ctypes.byref(cases[0][0]), 5, None) == _lib.FIE_E_ARG
 
 
+def test_lmhead_argument_errors():
+    """fie_sampler_lmhead_sample rejects, before any launch, a logits dtype other
+    than the model's fp16/bf16 and a hidden size that is not a multiple of 128."""
+    lib = _lib.load()
+    a = _args()
+    ws = _lib.Workspace(256, lib.fie_sampler_workspace_size(2, 100), 2, 100)
+    assert lib.fie_sampler_lmhead_sample(ctypes.byref(a), None, None, 128, ctypes.byref(ws), None) == _lib.FIE_E_ARG
+    assert b"fp16 or bf16" in lib.fie_sampler_last_error()
+    a.dtype = _lib.FIE_BF16
+    assert lib.fie_sampler_lmhead_sample(ctypes.byref(a), None, None, 100, ctypes.byref(ws), None) == _lib.FIE_E_ARG
+    assert b"multiple of 128" in lib.fie_sampler_last_error()
+    assert lib.fie_sampler_lmhead_sample(None, None, None, 128, ctypes.byref(ws), None) == _lib.FIE_E_ARG
+
+
 def test_zero_rows_is_a_no_op():
     lib = _lib.load()
     a = _args(rows=0)
