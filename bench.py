@@ -42,6 +42,8 @@ def parse():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--ring-mb", type=int, default=640)
+    ap.add_argument("--lmhead-dim", type=int, default=4096,
+                    help="hidden size of the fused lm_head measurement (0 to skip)")
     return ap.parse_args()
 
 
@@ -220,6 +222,63 @@ def cpu_baseline(w, seconds: float) -> dict:
                       f"{threads} threads on {cpu_model()}"}
 
 
+def time_lmhead(w, dev, H: int, steps: int = 20) -> dict:
+    """The fused lm_head (fie_sampler_lmhead_sample) against the two-step path it
+    replaces: the library GEMM torch.matmul runs for the model's output layer, then
+    fie_sampler_sample.  Same rows, parameters and histories as the headline
+    workload, fp16 operands.  Hidden states and weight rows are built so the logits
+    have the workload's peaked shape (-1.1 ln(rank + 1) + N(0, 0.5^2)): random
+    matrices would give flat logits, and every top-p row would take the full-row path."""
+    import torch
+    from fie_amd.batching.sampler import resolve_params
+    from fie_amd.kernel import FusedSampler
+
+    B, V = w.logits.shape
+    dt = torch.float16
+    g = torch.Generator(device=dev).manual_seed(20261201)
+    d = torch.randn(H, generator=g, device=dev)
+    d /= d.norm()
+    hidden = (d[None, :] + 0.01 * torch.randn(B, H, generator=g, device=dev) / H ** 0.5).to(dt)
+    ranks = torch.randperm(V, generator=g, device=dev).float()
+    scale = -1.1 * torch.log(ranks + 1.0)
+    weight = (scale[:, None] * d[None, :] + 0.5 * torch.randn(V, H, generator=g, device=dev)).to(dt)
+    hp = resolve_params(w.params, V, w.uniforms, w.contexts)
+    fs = FusedSampler(dev)
+    logits = torch.empty(B, V, dtype=dt, device=dev)
+    _, args, _, _ = fs.lmhead_step(hidden, weight, hp, logits)
+    exact_rows = 0
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            fn()
+        t1.record()
+        torch.cuda.synchronize()
+        return t0.elapsed_time(t1) * 1e3 / steps
+
+    fused_step = timed(lambda: fs.launch_lmhead(args, hidden, weight))
+    kernel = timed(lambda: fs.launch_lmhead(args, hidden, weight, kernel_only=True))
+    gemm = timed(lambda: torch.matmul(hidden, weight.T, out=logits))
+    scan = timed(lambda: fs.launch_stage(args, 1))
+    two_step = timed(lambda: (torch.matmul(hidden, weight.T, out=logits), fs.launch(args)))
+    out, _, _ = fs.step(logits, hp)
+    exact_rows = int(((out["status"] & 1) != 0).sum())
+    wbytes = V * H * 2
+    r = {"hidden_dim": H, "rows": B, "vocab": V, "dtype": "float16",
+         "fused_step_us": fused_step, "two_step_us": two_step,
+         "k_lmhead_us": kernel, "library_gemm_us": gemm, "k_scan_us": scan,
+         "k_lmhead_weight_gbs": wbytes / (kernel * 1e-6) / 1e9,
+         "k_lmhead_tflops": 2 * B * H * V / (kernel * 1e-6) / 1e12,
+         "exact_path_rows": exact_rows}
+    del weight, hidden, logits
+    torch.cuda.empty_cache()
+    return r
+
+
 def main() -> None:
     a = parse()
     if a.gpus != 1:
@@ -296,6 +355,11 @@ def main() -> None:
         del r
         torch.cuda.empty_cache()
     line["other_configs"] = others
+    if a.lmhead_dim:
+        try:
+            line["lmhead_fused"] = time_lmhead(w, dev, a.lmhead_dim)
+        except Exception as e:  # report, never hide the main line
+            line["lmhead_fused"] = f"failed: {e}"
     try:
         line["end_to_end_ms"] = end_to_end_ms(w, dev)
     except Exception as e:  # report, never hide the main line

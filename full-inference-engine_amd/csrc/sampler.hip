@@ -404,8 +404,8 @@ int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, vo
     return run_stage(P, FIE_STAGE_DEEP, st);
 }
 
-int fie_sampler_lmhead_sample(const fie_sampler_args* args, const void* hidden, const void* weight,
-                              int32_t hidden_dim, const fie_workspace* ws, void* stream)
+static int lmhead_run(const fie_sampler_args* args, const void* hidden, const void* weight, int32_t hidden_dim,
+                      const fie_workspace* ws, void* stream, bool whole)
 {
     if (!args) return fail(FIE_E_ARG, "args is NULL");
     if (args->dtype != FIE_F16 && args->dtype != FIE_BF16)
@@ -419,16 +419,30 @@ int fie_sampler_lmhead_sample(const fie_sampler_args* args, const void* hidden, 
     if (((uintptr_t)hidden % 16) != 0 || ((uintptr_t)weight % 16) != 0)
         return fail(FIE_E_ARG, "hidden and weight must be 16-byte aligned");
     hipStream_t st = (hipStream_t)stream;
-    rc = run_stage(P, FIE_STAGE_PREP, st);
-    if (rc != FIE_OK) return rc;
+    if (whole) {
+        rc = run_stage(P, FIE_STAGE_PREP, st);
+        if (rc != FIE_OK) return rc;
+    }
     const bool vec = vec_ok(args->logits, args->row_stride, 2);
     const bool longh = args->apply_penalties && args->max_row_hist > 65535;
     rc = args->dtype == FIE_F16 ? launch_lmhead<FIE_F16>(P, hidden, weight, hidden_dim, vec, longh, st)
                                 : launch_lmhead<FIE_BF16>(P, hidden, weight, hidden_dim, vec, longh, st);
-    if (rc != FIE_OK) return rc;
+    if (rc != FIE_OK || !whole) return rc;
     rc = run_stage(P, FIE_STAGE_FINISH, st);
     if (rc != FIE_OK) return rc;
     return run_stage(P, FIE_STAGE_DEEP, st);
+}
+
+int fie_sampler_lmhead_sample(const fie_sampler_args* args, const void* hidden, const void* weight,
+                              int32_t hidden_dim, const fie_workspace* ws, void* stream)
+{
+    return lmhead_run(args, hidden, weight, hidden_dim, ws, stream, true);
+}
+
+int fie_sampler_lmhead_stage(const fie_sampler_args* args, const void* hidden, const void* weight,
+                             int32_t hidden_dim, const fie_workspace* ws, void* stream)
+{
+    return lmhead_run(args, hidden, weight, hidden_dim, ws, stream, false);
 }
 
 int fie_sampler_stage(const fie_sampler_args* args, const fie_workspace* ws, int32_t stage, void* stream)

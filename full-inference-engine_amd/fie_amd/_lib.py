@@ -55,7 +55,7 @@ EXPORTS = (
     "fie_sampler_workspace_size", "fie_sampler_sample", "fie_sampler_stage",
     "fie_sampler_argmax", "fie_sampler_kept", "fie_sampler_cexp", "fie_sampler_last_error",
     "fie_sampler_sample_noalloc", "fie_sampler_uniforms", "fie_sampler_history_write",
-    "fie_sampler_lmhead_sample",
+    "fie_sampler_lmhead_sample", "fie_sampler_lmhead_stage",
 )
 SCRATCH_BYTES = 64 << 20
 
@@ -98,8 +98,9 @@ def bind(lib) -> None:
     lib.fie_sampler_sample_noalloc.argtypes = [ctypes.POINTER(SamplerArgs), _vp]
     lib.fie_sampler_uniforms.argtypes = [_vp, _vp, ctypes.c_int32, _vp]
     lib.fie_sampler_history_write.argtypes = [_vp, _vp, _vp, ctypes.c_int64, _vp]
-    lib.fie_sampler_lmhead_sample.argtypes = [ctypes.POINTER(SamplerArgs), _vp, _vp, ctypes.c_int32,
-                                              ctypes.POINTER(Workspace), _vp]
+    for name in ("fie_sampler_lmhead_sample", "fie_sampler_lmhead_stage"):
+        getattr(lib, name).argtypes = [ctypes.POINTER(SamplerArgs), _vp, _vp, ctypes.c_int32,
+                                       ctypes.POINTER(Workspace), _vp]
     lib.fie_sampler_last_error.restype = ctypes.c_char_p
     for name in EXPORTS:
         if name not in ("fie_sampler_workspace_size", "fie_sampler_last_error"):

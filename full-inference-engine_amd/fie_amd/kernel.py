@@ -294,13 +294,16 @@ class FusedSampler:
                                                  self._stream_ptr()), "fie_sampler_uniforms")
         return out
 
-    def launch_lmhead(self, args: SamplerArgs, hidden: torch.Tensor, weight: torch.Tensor) -> None:
+    def launch_lmhead(self, args: SamplerArgs, hidden: torch.Tensor, weight: torch.Tensor,
+                      kernel_only: bool = False) -> None:
         """The fused lm_head step: args.logits receives hidden @ weight.T and the
-        sampler runs on it (fie_sampler_lmhead_sample)."""
+        sampler runs on it (fie_sampler_lmhead_sample); with kernel_only, the fused
+        kernel alone (fie_sampler_lmhead_stage, for timing)."""
         ws = self.ensure_workspace(args.rows, args.vocab)
-        rc = self.lib.fie_sampler_lmhead_sample(ctypes.byref(args), hidden.data_ptr(), weight.data_ptr(),
-                                                hidden.shape[1], ctypes.byref(ws), self._stream_ptr())
-        _lib.check(rc, "fie_sampler_lmhead_sample")
+        fn = self.lib.fie_sampler_lmhead_stage if kernel_only else self.lib.fie_sampler_lmhead_sample
+        rc = fn(ctypes.byref(args), hidden.data_ptr(), weight.data_ptr(), hidden.shape[1], ctypes.byref(ws),
+                self._stream_ptr())
+        _lib.check(rc, "fie_sampler_lmhead_stage" if kernel_only else "fie_sampler_lmhead_sample")
 
     def lmhead_step(self, hidden: torch.Tensor, weight: torch.Tensor, hp: HostParams,
                     logits: torch.Tensor | None = None):

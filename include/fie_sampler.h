@@ -155,6 +155,13 @@ int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, vo
 int fie_sampler_lmhead_sample(const fie_sampler_args* args, const void* hidden, const void* weight,
                               int32_t hidden_dim, const fie_workspace* ws, void* stream);
 
+/* The fused kernel of fie_sampler_lmhead_sample alone (no penalty bucketing before it,
+   no selection after it), with the same arguments.  No counterpart in the reference:
+   it exists so a profiler or a benchmark can time the fused kernel by itself, after
+   one whole fie_sampler_lmhead_sample has prepared the workspace. */
+int fie_sampler_lmhead_stage(const fie_sampler_args* args, const void* hidden, const void* weight,
+                             int32_t hidden_dim, const fie_workspace* ws, void* stream);
+
 /* The kernels of fie_sampler_sample, one at a time, in this order (same args and
    workspace each time).  No counterpart in the reference: it exists so a profiler
    or a benchmark can time each kernel of the chain separately. */

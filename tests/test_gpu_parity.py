@@ -424,7 +424,8 @@ def _lmhead_case(rows, vocab, H, dtype, seed):
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("rows,vocab,H", [(5, 5000, 128), (70, 20001, 512), (130, 151936, 1024)])
+@pytest.mark.parametrize("rows,vocab,H", [(5, 5000, 128), (70, 20001, 512), (64, 8192, 256),
+                                          (130, 151936, 1024)])
 def test_lmhead_fused_matches_the_two_step_path(fs, dtype, rows, vocab, H):
     """fie_sampler_lmhead_sample: its logits are hidden @ weight.T to within one
     rounding of the model dtype (the fp32 sum's order differs from a library GEMM's),
