@@ -173,7 +173,11 @@ FIE_DEV uint32_t cand_target(int topk, int NT, bool greedy)
 {
     int c = kCandMin;                              // greedy rows: their top logprobs
     if (topk > 0) {
-        c = 2 * ((topk + NT - 1) / NT) + 4;
+        // a tile's share of the row's top k is about Poisson(lambda = k / tiles):
+        // lambda + 4 sqrt(lambda) + 4 leaves a tile holding more of them than its
+        // candidates (the row then takes the full-row path) below 1e-5 per tile
+        const float lam = (float)topk / (float)NT;
+        c = (int)__builtin_ceilf(lam + 4.0f * __builtin_sqrtf(lam)) + 4;
     } else if (!greedy) {
         // a top-p cut, min-p or a plain draw: as deep as the finish kernel can sort
         // (penalties on the chosen tokens flatten a row step after step)

@@ -88,26 +88,97 @@ class DeviceHistory:
 
     # ------------------------------------------------------------------ one step
     @staticmethod
-    def _note(slot: _Slot, new: np.ndarray, vocab: int) -> None:
-        """Token-0 bookkeeping of sampler.py:148,156-157 over appended ids."""
+    def _note(slot: _Slot, new: np.ndarray, vocab: int, base: int | None = None) -> None:
+        """Token-0 bookkeeping of sampler.py:148,156-157 over ids appended at
+        position `base` (the slot's length before them, by default)."""
         if not new.size:
             return
+        base = slot.length if base is None else base
         zeros = np.nonzero(new == 0)[0]
         big = np.nonzero(new >= vocab)[0]
         if slot.zero is None and zeros.size:
-            slot.zero = slot.length + int(zeros[0])
+            slot.zero = base + int(zeros[0])
         for p in big.tolist():
             t = int(new[p])
             if t not in slot.bigs:
                 slot.bigs.add(t)
-                if slot.zero is not None and slot.length + p > slot.zero:
+                if slot.zero is not None and base + p > slot.zero:
                     slot.late = True
 
     def update(self, contexts: list[list[int]], include: np.ndarray, request_ids: list[object],
                vocab: int):
         """Bring the penalised rows' stored contexts up to date.  Returns (starts,
         ends, hist_invalid or None, longest, write_dst, write_src): the rows'
-        ranges in ``ids`` and the appended tokens still to be written there."""
+        ranges in ``ids`` and the appended tokens still to be written there.
+
+        One pass per row decides each row's slot and gathers its appended ids into
+        one list; the range check and the token-0 scan then run once over all of
+        them, and the slots advance only after the check passes."""
+        rows = len(contexts)
+        picked = [request_ids[r] for r in range(rows) if include[r]]
+        if len(set(picked)) != len(picked):
+            # one request twice in a batch: rows see each other's appends in order
+            return self._update_rowwise(contexts, include, request_ids, vocab)
+        starts = np.zeros(rows, dtype=np.int64)
+        ends = np.zeros(rows, dtype=np.int64)
+        longest = 0
+        flat: list[int] = []
+        moved = []            # (slot, old length, new length, last id) of rows that grew
+        counts, bases = [], []
+        for r in range(rows):
+            if not include[r]:
+                continue
+            ctx = contexts[r]
+            n = len(ctx)
+            rid = request_ids[r]
+            slot = self.slots.get(rid)
+            if (slot is None or slot.vocab != vocab or n < slot.length
+                    or (slot.length and ctx[slot.length - 1] != slot.last)):
+                slot = self._new_slot(rid, n, vocab)
+            elif n > slot.cap:
+                self._grow(slot, n)
+            if n > slot.length:
+                flat.extend(ctx[slot.length:])
+                counts.append(n - slot.length)
+                bases.append(slot.start + slot.length)
+                moved.append((slot, slot.length, n, ctx[-1]))
+            starts[r] = slot.start
+            ends[r] = slot.start + n
+            if n > longest:
+                longest = n
+        if flat:
+            new = np.asarray(flat, dtype=np.int64)
+            if int(new.min()) < 0 or int(new.max()) >= 2**31:
+                raise ValueError("penalty context token ids must be in [0, 2**31)")
+            cnt = np.asarray(counts, dtype=np.int64)
+            first = np.cumsum(cnt) - cnt                      # each row's offset in `new`
+            dst = np.repeat(np.asarray(bases, dtype=np.int64) - first, cnt) + np.arange(new.size)
+            src = new.astype(np.int32)
+            odd = (new == 0) | (new >= vocab)
+            if odd.any():
+                seg = np.repeat(np.arange(cnt.size), cnt)
+                for i in np.unique(seg[odd]).tolist():
+                    slot, old, _, _ = moved[i]
+                    self._note(slot, new[first[i]:first[i] + cnt[i]], vocab, base=old)
+            for slot, _, n, last in moved:
+                slot.length = n
+                slot.last = int(last)
+        else:
+            dst = np.zeros(0, np.int64)
+            src = np.zeros(0, np.int32)
+        invalid = None
+        for r in range(rows):
+            if include[r]:
+                slot = self.slots[request_ids[r]]
+                if slot.bigs:
+                    if invalid is None:
+                        invalid = np.zeros(rows, dtype=np.int32)
+                    invalid[r] = len(slot.bigs) | ((1 << 30) if slot.late else 0)
+        return starts, ends, invalid, longest, dst, src
+
+    def _update_rowwise(self, contexts: list[list[int]], include: np.ndarray,
+                        request_ids: list[object], vocab: int):
+        """update() one row after another (a request that appears twice)."""
         rows = len(contexts)
         starts = np.zeros(rows, dtype=np.int64)
         ends = np.zeros(rows, dtype=np.int64)
