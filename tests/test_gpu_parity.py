@@ -457,3 +457,20 @@ def test_lmhead_rejects_what_it_cannot_run(fs):
         fs.lmhead_step(hidden, weight, hp)
     with pytest.raises(ValueError):
         fs.lmhead_step(hidden.float(), weight.float(), hp)
+
+
+def test_lmhead_long_history_counts(fs):
+    """The fused kernel's long-history variant (a row's history over 65535 ids: u32
+    penalty counts) matches the two-step path bit for bit."""
+    rows, vocab, H = 6, 9000, 256
+    hidden, weight, params, _, u = _lmhead_case(rows, vocab, H, torch.bfloat16, 77)
+    rng = np.random.default_rng(77)
+    params = [SamplingParams(temperature=0.9, top_p=0.8, repetition_penalty=1.3, frequency_penalty=0.01)] * rows
+    ctx = [list(rng.integers(0, 40, size=70_000)) if r == 2 else list(rng.integers(0, vocab, size=50))
+           for r in range(rows)]
+    hp = resolve_params(params, vocab, u, ctx)
+    assert hp.max_row_hist > 65535
+    out, _, _, logits = fs.lmhead_step(hidden.to(DEV), weight.to(DEV), hp)
+    two, _, _ = fs.step(logits, hp)
+    for name in ("tokens", "status", "cut_comp", "row_max", "kept_mass", "row_mass"):
+        np.testing.assert_array_equal(out[name], two[name], err_msg=name)
