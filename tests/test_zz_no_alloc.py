@@ -71,3 +71,43 @@ def test_noalloc_rejects_inputs_beyond_the_array():
     rc = fs.lib.fie_sampler_sample_noalloc(ctypes.byref(args), None)
     assert rc == _lib.FIE_E_WORKSPACE
     assert b"static scratch" in fs.lib.fie_sampler_last_error()
+
+
+def test_noalloc_replays_in_a_hip_graph():
+    """The no-allocation entry point captured once in a HIP graph and replayed over
+    fresh logits written (eagerly) into the same buffer: every replay matches an eager
+    fie_sampler_sample on the same logits.  The kernels record no memset and allocate
+    nothing, and every word a call reads is written earlier in that call."""
+    fs = FusedSampler(DEV)
+    w = W.make(3, rows=list(range(0, 256, 8)), device=DEV)          # 32 rows, penalties, all row kinds
+    B, V = w.logits.shape
+    hp = resolve_params(w.params, V, w.uniforms, w.contexts)
+    buf = fs.step_buffers(B, int(hp.hist_off[-1]))
+    buf.stage(hp)
+    stream = torch.cuda.current_stream(DEV)
+    buf.upload(stream)
+    logits = w.logits.to(DEV).clone()
+    args = fs.build_args(logits, buf, hp)
+    lib = fs.lib
+    _lib.check(lib.fie_sampler_sample_noalloc(ctypes.byref(args), ctypes.c_void_p(stream.cuda_stream)),
+               "fie_sampler_sample_noalloc")                          # resolves the array eagerly
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap = torch.cuda.current_stream(DEV)
+        _lib.check(lib.fie_sampler_sample_noalloc(ctypes.byref(args), ctypes.c_void_p(cap.cuda_stream)),
+                   "fie_sampler_sample_noalloc (captured)")
+    g = torch.Generator(device=DEV).manual_seed(3)
+    for rep in range(4):
+        print(f"  replay {rep}", flush=True)
+        perm = torch.randperm(V, generator=g, device=DEV)
+        logits.copy_(w.logits.to(DEV)[:, perm])                     # new values, same buffer
+        graph.replay()
+        buf.download(stream)
+        stream.synchronize()
+        got = {k: v.copy() for k, v in buf.outputs().items()}
+        fs.launch(args)
+        buf.download(stream)
+        stream.synchronize()
+        for name, want in buf.outputs().items():
+            np.testing.assert_array_equal(got[name], want, err_msg=f"{name} replay {rep}")
