@@ -68,10 +68,21 @@ struct FinSmem {
 };
 
 // Weight of a y-domain composite under rule R1: floor(cexp(y - m_t) 2^40) * C_t.
+// Both factors are at most 2^40; split at bit 24 they give four products of operands
+// below 2^24, which the 24-bit multiplier forms at full rate (a 64 x 64-bit product
+// takes eight quarter-rate 32-bit multiplies).  The sum is the exact product.
 FIE_DEV u128 weight_of(const FinSmem& S, float y, uint32_t idx)
 {
     const int slot = idx == 0 ? 0 : 1 + (int)(idx / kTile);
-    return (u128)tok_weight(y, S.mt[slot]) * S.ct[slot];
+    const float w = weight40(y - S.mt[slot]);              // an integer below 2^41, as a float
+    const float wh = __builtin_floorf(w * 0x1p-24f);       // exact: w has 24 significant bits
+    const uint32_t w1 = (uint32_t)wh & 0x1FFFFu;
+    const uint32_t w0 = (uint32_t)(w - wh * 0x1p24f) & 0xFFFFFFu;
+    const uint64_t c = S.ct[slot];
+    const uint32_t c0 = (uint32_t)c & 0xFFFFFFu, c1 = (uint32_t)(c >> 24) & 0x1FFFFu;
+    const uint64_t p00 = (uint64_t)w0 * c0, p01 = (uint64_t)w0 * c1;
+    const uint64_t p10 = (uint64_t)w1 * c0, p11 = (uint64_t)w1 * c1;
+    return (u128)p00 + ((u128)(p01 + p10) << 24) + ((u128)p11 << 48);
 }
 
 FIE_DEV u128 comp_weight(const FinSmem& S, uint64_t c)
