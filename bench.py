@@ -2,8 +2,8 @@
 
 One step = one fused sampler call (penalties, temperature, top-k / top-p / min-p,
 draw, logprobs) over one [B, V] logits batch already resident in HBM, with the
-step's parameters and penalty histories resident too: the three kernels k_prep,
-k_scan and k_finish.  Logits rotate through enough distinct buffers (> 512 MB) that the 256 MB
+step's parameters and penalty histories resident too: the four kernels k_prep,
+k_scan, k_finish and k_deep (idle when no row needs the full-row path).  Logits rotate through enough distinct buffers (> 512 MB) that the 256 MB
 Infinity Cache cannot serve them.
 
 Prints one JSON line: rows/s and us/step for the headline config, the roofline of
