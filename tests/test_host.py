@@ -166,6 +166,31 @@ def test_device_history_tracks_appends_rebuilds_and_growth():
             assert dst.size == sum(include)                            # only the appends moved
 
 
+def test_device_history_duplicate_rows_and_rejected_ids():
+    """A request twice in one batch takes the row-by-row update: each of its rows reads
+    the request's whole context.  An id outside [0, 2**31) raises before any slot moves:
+    the next valid update appends exactly as if the failed one never happened."""
+    import torch
+    from fie_amd.batching.history import DeviceHistory
+
+    vocab = 50
+    h = DeviceHistory(torch.device("cpu"), capacity=64)
+    a_ctx, b_ctx = [1, 2, 3], [4, 0, 60]
+    starts, ends, invalid, _, dst, src = h.update([a_ctx, b_ctx, a_ctx], np.ones(3, bool), ["a", "b", "a"], vocab)
+    h.ids[torch.from_numpy(dst)] = torch.from_numpy(src)
+    for r, ctx in enumerate([a_ctx, b_ctx, a_ctx]):
+        np.testing.assert_array_equal(h.ids[starts[r]:ends[r]].numpy(), np.array(ctx, dtype=np.int32))
+    assert invalid is not None and invalid[1] == 1 | (1 << 30) and invalid[0] == invalid[2] == 0
+    before = {rid: (s.start, s.length, s.last) for rid, s in h.slots.items()}
+    with pytest.raises(ValueError):
+        h.update([a_ctx + [5], b_ctx + [-1]], np.ones(2, bool), ["a", "b"], vocab)
+    assert {rid: (s.start, s.length, s.last) for rid, s in h.slots.items()} == before
+    starts, ends, _, _, dst, src = h.update([a_ctx + [5], b_ctx + [6]], np.ones(2, bool), ["a", "b"], vocab)
+    assert dst.size == 2
+    h.ids[torch.from_numpy(dst)] = torch.from_numpy(src)
+    np.testing.assert_array_equal(h.ids[starts[1]:ends[1]].numpy(), np.array(b_ctx + [6], dtype=np.int32))
+
+
 # ---------------------------------------------------------------- the adapter's calls
 class _NoKernels(BatchedSampler):
     """BatchedSampler with its host state only (the constructor's device setup is
