@@ -32,6 +32,10 @@ class _Slot:
 class DeviceHistory:
     """Per-request contexts in one int32 device array (a bump arena)."""
 
+    # set once any stored context holds an id >= vocab: only then do rows need the
+    # out-of-vocabulary scan of update()
+    _with_bigs = False
+
     def __init__(self, device: torch.device, capacity: int = 1 << 20):
         self.device = device
         self.ids = torch.empty(capacity, dtype=torch.int32, device=device)
@@ -102,6 +106,7 @@ class DeviceHistory:
             t = int(new[p])
             if t not in slot.bigs:
                 slot.bigs.add(t)
+                DeviceHistory._with_bigs = True
                 if slot.zero is not None and base + p > slot.zero:
                     slot.late = True
 
@@ -115,37 +120,44 @@ class DeviceHistory:
         one list; the range check and the token-0 scan then run once over all of
         them, and the slots advance only after the check passes."""
         rows = len(contexts)
-        picked = [request_ids[r] for r in range(rows) if include[r]]
+        sel = np.flatnonzero(include).tolist()
+        picked = [request_ids[r] for r in sel]
         if len(set(picked)) != len(picked):
             # one request twice in a batch: rows see each other's appends in order
             return self._update_rowwise(contexts, include, request_ids, vocab)
-        starts = np.zeros(rows, dtype=np.int64)
-        ends = np.zeros(rows, dtype=np.int64)
+        starts_l = [0] * rows
+        ends_l = [0] * rows
         longest = 0
         flat: list[int] = []
         moved = []            # (slot, old length, new length, last id) of rows that grew
         counts, bases = [], []
-        for r in range(rows):
-            if not include[r]:
-                continue
+        get = self.slots.get
+        extend, c_append, b_append, m_append = flat.extend, counts.append, bases.append, moved.append
+        for r, rid in zip(sel, picked):
             ctx = contexts[r]
             n = len(ctx)
-            rid = request_ids[r]
-            slot = self.slots.get(rid)
-            if (slot is None or slot.vocab != vocab or n < slot.length
-                    or (slot.length and ctx[slot.length - 1] != slot.last)):
+            slot = get(rid)
+            if slot is None:
                 slot = self._new_slot(rid, n, vocab)
-            elif n > slot.cap:
-                self._grow(slot, n)
-            if n > slot.length:
-                flat.extend(ctx[slot.length:])
-                counts.append(n - slot.length)
-                bases.append(slot.start + slot.length)
-                moved.append((slot, slot.length, n, ctx[-1]))
-            starts[r] = slot.start
-            ends[r] = slot.start + n
+            else:
+                ln = slot.length
+                if slot.vocab != vocab or n < ln or (ln and ctx[ln - 1] != slot.last):
+                    slot = self._new_slot(rid, n, vocab)
+                elif n > slot.cap:
+                    self._grow(slot, n)
+            ln = slot.length
+            st = slot.start
+            if n > ln:
+                extend(ctx[ln:])
+                c_append(n - ln)
+                b_append(st + ln)
+                m_append((slot, ln, n, ctx[-1]))
+            starts_l[r] = st
+            ends_l[r] = st + n
             if n > longest:
                 longest = n
+        starts = np.array(starts_l, dtype=np.int64)
+        ends = np.array(ends_l, dtype=np.int64)
         if flat:
             new = np.asarray(flat, dtype=np.int64)
             if int(new.min()) < 0 or int(new.max()) >= 2**31:
@@ -167,9 +179,10 @@ class DeviceHistory:
             dst = np.zeros(0, np.int64)
             src = np.zeros(0, np.int32)
         invalid = None
-        for r in range(rows):
-            if include[r]:
-                slot = self.slots[request_ids[r]]
+        if self._with_bigs:
+            slots = self.slots
+            for r, rid in zip(sel, picked):
+                slot = slots[rid]
                 if slot.bigs:
                     if invalid is None:
                         invalid = np.zeros(rows, dtype=np.int32)

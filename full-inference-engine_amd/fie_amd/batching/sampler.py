@@ -14,6 +14,7 @@ counters.
 
 from __future__ import annotations
 
+import operator
 import os
 from collections import OrderedDict
 from dataclasses import dataclass
@@ -72,6 +73,53 @@ def pack_history(contexts: list[list[int]], include: np.ndarray, vocab: int):
 _EMPTY = np.zeros(0, dtype=np.int64)
 
 
+class ParamTable:
+    """Per-row columns of a batch's SamplingParams, from one pass over the objects.
+
+    A decode loop passes the same SamplingParams objects step after step (each
+    request keeps its own); the last table is reused when the batch holds exactly the
+    same objects in the same order.  The table keeps those objects alive, so an
+    identity match cannot be a new object at a recycled address."""
+
+    __slots__ = ("objs", "greedy", "pen", "temps", "top_k", "top_p", "min_p", "lp",
+                 "rep", "pres", "freq", "seeded", "seeds")
+
+    def __init__(self, params: list[SamplingParams]):
+        self.objs = list(params)
+        rows = [(p.greedy, p.has_penalties, p.temperature, p.top_k, p.top_p, p.min_p,
+                 -1 if p.logprobs is None else p.logprobs, p.repetition_penalty,
+                 p.presence_penalty, p.frequency_penalty,
+                 p.seed is not None, 0 if p.seed is None else p.seed) for p in params]
+        cols = list(zip(*rows)) if rows else [()] * 12
+        self.greedy = np.array(cols[0], dtype=bool)
+        self.pen = np.array(cols[1], dtype=bool)
+        self.temps = np.array(cols[2], dtype=np.float64)
+        self.top_k = np.array(cols[3], dtype=np.int64)
+        self.top_p = np.array(cols[4], dtype=np.float64)
+        self.min_p = np.array(cols[5], dtype=np.float64)
+        self.lp = np.array(cols[6], dtype=np.int32)
+        self.rep = np.array(cols[7], dtype=np.float32)
+        self.pres = np.array(cols[8], dtype=np.float32)
+        self.freq = np.array(cols[9], dtype=np.float32)
+        self.seeded = np.array(cols[10], dtype=bool)
+        self.seeds = np.array(cols[11], dtype=np.uint64) if rows else np.zeros(0, np.uint64)
+
+    def matches(self, params: list[SamplingParams]) -> bool:
+        objs = self.objs
+        return len(params) == len(objs) and all(map(operator.is_, params, objs))
+
+
+_last_table: list[ParamTable | None] = [None]
+
+
+def param_table(params: list[SamplingParams]) -> ParamTable:
+    t = _last_table[0]
+    if t is None or not t.matches(params):
+        t = ParamTable(params)
+        _last_table[0] = t
+    return t
+
+
 def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarray | None,
                    contexts: list[list[int]] | None, rng: np.ndarray | None = None,
                    history: DeviceHistory | None = None,
@@ -84,14 +132,8 @@ def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarra
     rows = len(params)
     if uniforms is None:
         uniforms = np.zeros(rows, dtype=np.float64)
-    greedy = np.fromiter((p.greedy for p in params), dtype=bool, count=rows)
-    pen = np.fromiter((p.has_penalties for p in params), dtype=bool, count=rows)
-    temps = np.fromiter((p.temperature for p in params), dtype=np.float64, count=rows)
-    top_k = np.fromiter((p.top_k for p in params), dtype=np.int64, count=rows)
-    top_p = np.fromiter((p.top_p for p in params), dtype=np.float64, count=rows)
-    min_p = np.fromiter((p.min_p for p in params), dtype=np.float64, count=rows)
-    lp = np.fromiter((-1 if p.logprobs is None else p.logprobs for p in params),
-                     dtype=np.int32, count=rows)
+    t = param_table(params)
+    greedy, pen, temps, top_k, top_p, min_p = t.greedy, t.pen, t.temps, t.top_k, t.top_p, t.min_p
     apply = bool(pen.any()) and contexts is not None
     ends = dst = src = None
     if apply and history is not None and request_ids is not None:
@@ -107,11 +149,11 @@ def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarra
         top_p=np.where((top_p < 1.0) & ~greedy, top_p, 1.0).astype(np.float32),
         min_p=np.where((min_p > 0.0) & ~greedy, min_p, 0.0).astype(np.float32),
         flags=(greedy.astype(np.int32) * FLAG_GREEDY + pen.astype(np.int32) * FLAG_PENALTY),
-        logprobs=lp,
+        logprobs=t.lp,
         uniform=np.ascontiguousarray(uniforms, dtype=np.float64),
-        rep=np.fromiter((p.repetition_penalty for p in params), np.float32, count=rows),
-        pres=np.fromiter((p.presence_penalty for p in params), np.float32, count=rows),
-        freq=np.fromiter((p.frequency_penalty for p in params), np.float32, count=rows),
+        rep=t.rep,
+        pres=t.pres,
+        freq=t.freq,
         hist_off=offsets,
         hist_ids=ids,
         apply_penalties=apply,
@@ -174,16 +216,18 @@ class BatchedSampler:
         stream at its next position, the shared stream in row order otherwise
         (greedy rows draw nothing)."""
         rows = len(params)
+        t = param_table(params)
         keys = np.zeros((rows, 3), dtype=np.uint64)
-        for r, p in enumerate(params):
-            if p.greedy:
-                continue
-            if p.seed is None:
-                self._shared_draws += 1
-                keys[r] = (self._shared_key, SHARED_STREAM, self._shared_draws)
-            else:
-                rid = request_ids[r] if request_ids is not None else r
-                keys[r] = (p.seed, SEEDED_STREAM, self._next_draw(rid))
+        shared = np.nonzero(~t.greedy & ~t.seeded)[0]
+        if shared.size:
+            keys[shared, 0] = self._shared_key
+            keys[shared, 1] = SHARED_STREAM
+            keys[shared, 2] = np.arange(self._shared_draws + 1, self._shared_draws + 1 + shared.size,
+                                        dtype=np.uint64)
+            self._shared_draws += int(shared.size)
+        for r in np.nonzero(~t.greedy & t.seeded)[0].tolist():
+            rid = request_ids[r] if request_ids is not None else r
+            keys[r] = (int(t.seeds[r]), SEEDED_STREAM, self._next_draw(rid))
         return keys
 
     # ------------------------------------------------------------------ the step
