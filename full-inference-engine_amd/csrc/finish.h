@@ -208,13 +208,14 @@ FIE_DEV SelResult lds_select(FinSmem& S, int n, const Pred pr, u128 g)
 // ---------------------------------------------------------------- full-row passes
 // Visit every token of the row once, re-reading it from memory: f(y, idx) with each
 // token's scaled (penalised) logit, token 0 with its settled value.  The row streams
-// in kChunk-token chunks, the next chunk's loads in flight while one is processed
-// (a pass is bound by its per-token instructions: deeper prefetch measured no
-// faster).  A penalised row's counts come
+// in kChunk-token chunks through a ring of kPassDepth register buffers, the next
+// chunks' loads in flight while one is processed.  A pass is bound by its per-token
+// instructions: the third buffer gains 3% on many full-row rows at once and nothing
+// on a single one.  A penalised row's counts come
 // from k_prep's span bucket, loaded with the chunk (one id per thread: kBucketCap ==
 // kFinThreads), so counting never waits on a dependent load; a span whose bucket
 // overflowed is counted from the whole history instead.
-constexpr int kPassDepth = 2;
+constexpr int kPassDepth = 3;
 static_assert(kBucketCap == kFinThreads && kSpan == 2 * kChunk, "bucket entries per thread, chunks per span");
 
 template <int DT, bool VEC, class F>
@@ -240,9 +241,14 @@ FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, 
         const int lo = c * kChunk;
 #pragma unroll
         for (int j = 0; j < NL; ++j) b[j] = load_group<DT, VEC>(rowp, lo + (j * kFinThreads + tid) * EPL, V);
-        if (pen) of = P.w.bk[((size_t)row * P.NS + lo / kSpan) * kBucketCap + tid];
+        if (pen) {
+            // a chunk past the row's end (the ring's tail) reads the last span's entry, unused
+            const int sp = lo / kSpan < P.NS ? lo / kSpan : P.NS - 1;
+            of = P.w.bk[((size_t)row * P.NS + sp) * kBucketCap + tid];
+        }
     };
     auto count = [&](uint32_t of, int lo, int hi) {
+        if (lo >= V) return;                                     // uniform: no token to count
         for (int i = tid; i < kChunk / 4; i += kFinThreads) ((uint4*)S.cnt)[i] = make_uint4(0, 0, 0, 0);
         __syncthreads();
         const uint32_t nb = S.snb[lo / kSpan];
@@ -261,37 +267,37 @@ FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, 
 #pragma unroll
     for (int q = 0; q < D; ++q)
         if (q < nch) issue(buf[q], bof[q], q);
-    for (int c = 0; c < nch; ++c) {
-        // buf[0] holds chunk c, buf[q] chunk c + q
-        const int lo = c * kChunk, hi = min(lo + kChunk, V);
-        if (pen) count(bof[0], lo, hi);
+    // a ring of D buffers in fixed roles (no register copies, which would wait on
+    // loads still in flight): buffer q holds chunk c0 + q while the others load.
+    // Past the row's end the loads read nothing and every token fails idx < V.
+    for (int c0 = 0; c0 < nch; c0 += D) {
 #pragma unroll
-        for (int j = 0; j < NL; ++j) {
-            const int e0 = lo + (j * kFinThreads + tid) * EPL;
+        for (int q = 0; q < D; ++q) {
+            const int c = c0 + q;
+            const int lo = c * kChunk, hi = min(lo + kChunk, V);
+            if (pen) count(bof[q], lo, hi);
 #pragma unroll
-            for (int e = 0; e < EPL; ++e) {
-                const int idx = e0 + e;
-                if (idx >= V || idx == 0) continue;
-                float x = lane_get<DT>(buf[0][j], e);
-                if (pen) {
-                    const uint32_t cc = S.cnt[idx - lo];
-                    if (cc) x = penalize(x, rep, pres, freq, cc);
+            for (int j = 0; j < NL; ++j) {
+                const int e0 = lo + (j * kFinThreads + tid) * EPL;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const int idx = e0 + e;
+                    if (idx >= V || idx == 0) continue;
+                    float x = lane_get<DT>(buf[q][j], e);
+                    if (pen) {
+                        const uint32_t cc = S.cnt[idx - lo];
+                        if (cc) x = penalize(x, rep, pres, freq, cc);
+                    }
+                    float y;
+                    if (s == 1.0f) y = x + 0.0f;
+                    else if (mark && markstein_ok(x)) y = div_markstein(x, s, rs) + 0.0f;
+                    else y = scaled(x, s);
+                    f(y, (uint32_t)idx);
                 }
-                float y;
-                if (s == 1.0f) y = x + 0.0f;
-                else if (mark && markstein_ok(x)) y = div_markstein(x, s, rs) + 0.0f;
-                else y = scaled(x, s);
-                f(y, (uint32_t)idx);
             }
+            if (pen) __syncthreads();
+            issue(buf[q], bof[q], c + D);
         }
-        if (pen) __syncthreads();
-#pragma unroll
-        for (int q = 0; q + 1 < D; ++q) {
-#pragma unroll
-            for (int j = 0; j < NL; ++j) buf[q][j] = buf[q + 1][j];
-            bof[q] = bof[q + 1];
-        }
-        if (c + D < nch) issue(buf[D - 1], bof[D - 1], c + D);
     }
     __syncthreads();
 }
