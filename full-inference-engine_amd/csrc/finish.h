@@ -46,15 +46,18 @@ struct SelResult {
 struct FinSmem {
     uint64_t cand[kGCap];                       // candidates or a gathered key range
     uint32_t pc[kPassBins];                     // full-row pass: counts per bin
-    uint64_t pm_lo[kPassBins], pm_hi[kPassBins];// full-row pass: mass per bin
+    union {
+        uint64_t pm_lo[kPassBins];              // full-row pass: mass per bin (low limb)
+        float pmf[kPassBins];                   // candidate narrowing: float mass per bin
+    };
+    uint64_t pm_hi[kPassBins];                  // full-row pass: mass per bin (high limb)
     uint32_t cnt[kChunk];                       // penalty counts of one chunk
     uint32_t snb[kMaxSpans];                    // history ids per span (k_prep), of a pass's row
     uint32_t hc[256];                           // LDS selection: counts per digit
     uint64_t hm_lo[256], hm_hi[256];            // LDS selection: mass per digit
     float mt[kMaxTiles + 1];                    // tile maxima of y (slot 0 = token 0)
     uint64_t ct[kMaxTiles + 1];                 // tile scales C_t
-    uint64_t tmc[kMaxTiles];                    // tile maxima composites (x keys)
-    uint32_t coff[kMaxTiles + 1];               // candidate offsets per tile
+    uint32_t nc[kMaxTiles];                     // candidates per tile
     uint64_t red64[16];
     u128 red128[16];
     uint32_t red32[32];
@@ -796,58 +799,188 @@ FIE_DEV bool q1_keeps(FinSmem& S, const KParams& P, int row)
     return mine == wmax && !late;
 }
 
-// The row's candidates from every tile as y-domain composites, token 0 included:
-// those whose key exceeds `safe` (the complete region) into S.cand in any order,
-// at most kGCap of them.  Returns how many there are (possibly more than were
-// stored); S.cmax receives the largest composite of all n.
-FIE_DEV int load_candidates(FinSmem& S, const KParams& P, int row, int NT, int n, float s,
-                            uint32_t k0, uint32_t safe)
+// ---------------------------------------------------------------- candidates
+// A tile's candidates sit in kCapW (= one wave) slots of the partials, the first
+// S.nc[t] of them valid: wave w reads tile t = t0 + w + kFinWaves q with one 512-byte
+// load, Q tiles per wave held at once (Q = 10: rows of up to 80 tiles in one round
+// trip; kReloadQ where registers are short).
+constexpr int kFinWaves = kFinThreads / 64;
+constexpr int kReloadQ = 5;
+static_assert(kCapW == 64, "one tile's candidate slots per wave");
+static_assert(kMaxTiles < kFinThreads, "the last thread is free for token 0");
+
+// Float mass of a token y relative to the row maximum M: rule R1's weight / 2^80 up
+// to the floors of R1 and the exponentials' rounding (used only to narrow).
+FIE_DEV float approx_mass(float y, float M) { return __expf(y - M); }
+
+// The x-domain candidate slot as a y-domain composite.
+FIE_DEV uint64_t cand_y(uint64_t xc, float s)
 {
-    constexpr int kPer = 4;                      // candidates per thread per batch
-    if (threadIdx.x == 0) { S.n = 0; S.cmax = 0; }
-    __syncthreads();
-    uint64_t best = 0;
-    for (int base = 0; base < n; base += kPer * kFinThreads) {
-        // the tiles of this thread's elements first (LDS), then all their loads in
-        // flight together, then the conversions
-        uint64_t xc[kPer];
+    return comp_key(fkey(y_of_xkey(comp_k(xc), s)), comp_idx(xc));
+}
+
+// Q held y-domain composites per thread (those with ok set): the largest is tracked;
+// those whose key exceeds `safe` join S.cand (at most kGCap stored, all counted in
+// S.n: one LDS atomic per wave) and, with `bins`, the count and float mass of their
+// d-bin.  Called by whole waves.
+template <int Q>
+FIE_DEV void cand_commit(FinSmem& S, const uint64_t (&cv)[Q], const bool (&ok)[Q], uint32_t safe,
+                         uint64_t& best, bool bins, float M)
+{
+    uint32_t keep = 0, k = 0;
 #pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            const int i = base + q * kFinThreads + threadIdx.x;
-            xc[q] = 0;
-            if (i < n - 1) {
-                int lo = 0, hi = NT - 1;         // tile t with coff[t] <= i < coff[t+1]
-                while (lo < hi) {
-                    const int mid = (lo + hi + 1) >> 1;
-                    if (S.coff[mid] <= (uint32_t)i) lo = mid;
-                    else hi = mid - 1;
-                }
-                xc[q] = P.w.cand[((size_t)row * NT + lo) * kCapW + (i - S.coff[lo])];
-            }
-        }
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            const int i = base + q * kFinThreads + threadIdx.x;
-            if (i >= n) continue;
-            const uint64_t c = i == n - 1 ? comp_key(k0, 0)
-                                          : comp_key(fkey(y_of_xkey(comp_k(xc[q]), s)), comp_idx(xc[q]));
-            best = c > best ? c : best;
-            if (comp_k(c) > safe) {
-                const uint32_t at = atomicAdd(&S.n, 1u);
-                if (at < (uint32_t)kGCap) S.cand[at] = c;
-            }
+    for (int q = 0; q < Q; ++q) {
+        if (ok[q]) best = cv[q] > best ? cv[q] : best;
+        if (ok[q] && comp_k(cv[q]) > safe) {
+            keep |= 1u << q;
+            ++k;
         }
     }
+    uint32_t wt;
+    uint32_t at = dwave_excl_scan_u32(k, &wt);
+    if (wt == 0) return;                          // uniform
+    uint32_t base = 0;
+    if ((threadIdx.x & 63) == 0) base = atomicAdd(&S.n, wt);
+    at += (uint32_t)__shfl((int)base, 0, 64);
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        if (!((keep >> q) & 1u)) continue;
+        if (at < (uint32_t)kGCap) S.cand[at] = cv[q];
+        ++at;
+        if (bins) {
+            const float y = key_to_float(comp_k(cv[q]));
+            const int b = dbin_y(M, y);
+            atomicAdd(&S.pc[b], 1u);
+            atomicAdd(&S.pmf[b], approx_mass(y, M));
+        }
+    }
+}
+
+// Tiles t0 + w + kFinWaves q (q < Q) of the row, and token 0 (composite z0) on the
+// last thread when `with0`: load, convert, commit.
+template <int Q>
+FIE_DEV void cand_batch(FinSmem& S, const KParams& P, int row, int NT, int t0, float s, uint32_t safe,
+                        uint64_t& best, bool bins, float M, bool with0, uint64_t z0)
+{
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint64_t cv[Q + 1];
+    bool ok[Q + 1];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int t = t0 + wave + kFinWaves * q;
+        ok[q] = t < NT && (uint32_t)lane < S.nc[t];
+        cv[q] = ok[q] ? P.w.cand[((size_t)row * NT + t) * kCapW + lane] : 0ull;
+    }
+#pragma unroll
+    for (int q = 0; q < Q; ++q) cv[q] = ok[q] ? cand_y(cv[q], s) : 0ull;
+    ok[Q] = with0 && tid == kFinThreads - 1;
+    cv[Q] = z0;
+    cand_commit(S, cv, ok, safe, best, bins, M);
+}
+
+// The row's candidates from every tile, token 0 (the last thread) included: those
+// whose key exceeds `safe` into S.cand in any order, at most kGCap of them.  Returns
+// how many there are (possibly more than were stored); S.cmax receives the largest
+// composite of all.  Needs S.nc.
+FIE_DEV int load_candidates(FinSmem& S, const KParams& P, int row, int NT, float s, uint32_t k0, uint32_t safe)
+{
+    const int tid = threadIdx.x;
+    if (tid == 0) { S.n = 0; S.cmax = 0; }
+    __syncthreads();
+    uint64_t best = 0;
+    for (int t0 = 0; t0 < NT; t0 += kFinWaves * kReloadQ)
+        cand_batch<kReloadQ>(S, P, row, NT, t0, s, safe, best, false, 0.0f, t0 == 0, comp_key(k0, 0));
     best = wave_max_u64(best);
-    if ((threadIdx.x & 63) == 0 && best) atomicMax((unsigned long long*)&S.cmax, (unsigned long long)best);
+    if ((tid & 63) == 0 && best) atomicMax((unsigned long long*)&S.cmax, (unsigned long long)best);
     __syncthreads();
     const int m = (int)S.n;
     __syncthreads();
     return m;
 }
 
+FIE_DEV float wave_incl_scan_f32(float v)
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const float u = __shfl_up(v, d, 64);
+        if (lane >= d) v += u;
+    }
+    return v;
+}
+
+// narrow_candidates for a row binned as its candidates were taken (S.pc counts,
+// S.pmf float masses): the count criterion is exact; the mass criterion asks the
+// float prefix to exceed g by a margin (2^-9 relative, 2^-26 absolute, in units of
+// 2^80) that covers the float sums' rounding and the floors of rule R1, so the
+// prefix it picks holds exact mass above g.  Should a crossing still fall past the
+// prefix, the exact selection finds no element there and reloads every candidate.
+FIE_DEV int narrow_binned(FinSmem& S, int nv, float M, int cnt, u128 g)
+{
+    constexpr int per = kPassBins / kFinThreads;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float target = (float)(u128_to_double(g) * 0x1p-80 * (1.0 + 0x1p-9) + 0x1p-26);
+    uint32_t c[per], cs = 0;
+    float m[per], ms = 0.0f;
+#pragma unroll
+    for (int q = 0; q < per; ++q) {
+        c[q] = S.pc[tid * per + q];
+        m[q] = S.pmf[tid * per + q];
+        cs += c[q];
+        ms += m[q];
+    }
+    const uint32_t ci = wave_incl_scan_u32(cs);
+    const float mi = wave_incl_scan_f32(ms);
+    if (lane == 63) {
+        S.red32[wave] = ci;
+        S.red32[kFinWaves + wave] = __float_as_uint(mi);
+    }
+    if (tid == 0) {
+        S.ibin = cnt > 0 ? -1 : 0;
+        S.flag = -1;
+        S.bcnt = 0;
+    }
+    __syncthreads();
+    uint32_t cb = ci - cs;
+    float mb = mi - ms;
+    for (int w = 0; w < wave; ++w) {
+        cb += S.red32[w];
+        mb += __uint_as_float(S.red32[kFinWaves + w]);
+    }
+    uint32_t crun = cb;
+    float mrun = mb;
+#pragma unroll
+    for (int q = 0; q < per; ++q) {
+        const int b = tid * per + q;
+        if (cnt > 0 && crun < (uint32_t)cnt && crun + c[q] >= (uint32_t)cnt) S.ibin = b;
+        if (!(mrun > target) && mrun + m[q] > target) atomicMax(&S.flag, b);
+        crun += c[q];
+        mrun += m[q];
+    }
+    __syncthreads();
+    const int bc = S.ibin, bm = S.flag;
+    if (bc < 0 || bm < 0) return nv;
+    const int bs = bc > bm ? bc : bm;
+    constexpr int kStage = kChunk / 2;           // S.cnt holds this many composites
+    uint64_t* tmp = (uint64_t*)S.cnt;
+    for (int i = tid; i < nv; i += kFinThreads) {
+        const uint64_t x = S.cand[i];
+        if (dbin_key(M, comp_k(x)) <= bs) {
+            const uint32_t at = atomicAdd(&S.bcnt, 1u);
+            if (at < (uint32_t)kStage) tmp[at] = x;
+        }
+    }
+    __syncthreads();
+    const int k = (int)S.bcnt;
+    if (k > kStage || k >= nv) return nv;
+    for (int i = tid; i < k; i += kFinThreads) S.cand[i] = tmp[i];
+    __syncthreads();
+    return k;
+}
+
 // ---------------------------------------------------------------- sorted candidates
 constexpr int kSortMax = kGCap;    // candidates sorted in LDS, at most
+constexpr int kRankSort = 256;     // up to this many sort by rank (two or more threads each), more by bitonic merges
 
 // v of lane (lane ^ J): DPP moves inside rows of 16 lanes (quad permutes for 1 and
 // 2, row shifts by 4 and 8 selected by the lane's bit), a swizzle inside 32 lanes
@@ -921,6 +1054,40 @@ FIE_DEV void wave_bitonic(uint64_t* c, int base, int k0, int k1)
 FIE_DEV void sort_desc(FinSmem& S, int n)
 {
     const int tid = threadIdx.x, wave = tid >> 6;
+    if (n <= kRankSort) {
+        // a rank sort: each composite's place is the number of larger ones (they are
+        // distinct), counted over broadcast LDS reads by F threads per composite, each
+        // over one F-th of the list; partial counts meet in S.pc
+        int np = 64;
+        while (np < n) np <<= 1;
+        const int F = kFinThreads / np;
+        const int i = tid & (np - 1), h = tid / np;
+        const bool have = i < n;
+        const uint64_t e = have ? S.cand[i] : 0ull;
+        const int part = ((n + F - 1) / F + 1) & ~1;          // even: 16-byte reads stay aligned
+        const int jlo = min(h * part, n), jhi = min(jlo + part, n);
+        uint32_t r = 0;
+        if (have) {
+            int j = jlo;
+            for (; j + 8 <= jhi; j += 8) {
+                ulonglong2 p[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) p[u] = *(const ulonglong2*)&S.cand[j + 2 * u];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) r += (p[u].x > e ? 1u : 0u) + (p[u].y > e ? 1u : 0u);
+            }
+            for (; j < jhi; ++j) r += S.cand[j] > e ? 1u : 0u;
+            if (h) S.pc[tid] = r;
+        }
+        __syncthreads();
+        if (have && !h) {
+            for (int k = 1; k < F; ++k) r += S.pc[k * np + i];
+            S.cand[r] = e;
+        }
+        for (int k = n + tid; k < 128; k += kFinThreads) S.cand[k] = 0;   // as the merge sort pads
+        __syncthreads();
+        return;
+    }
     int N = 128;
     while (N < n) N <<= 1;
     for (int i = n + tid; i < N; i += kFinThreads) S.cand[i] = 0;
@@ -944,88 +1111,85 @@ FIE_DEV void sort_desc(FinSmem& S, int n)
     __syncthreads();
 }
 
-// Number of leading sorted candidates whose key satisfies key > t (strict) or
-// key >= t: a prefix, since the order is key-major.
-FIE_DEV int sorted_prefix(FinSmem& S, int n, uint32_t t, bool strict)
+// One thread's chunk [lo, hi) of the sorted candidates S.cand[0, nv): the mass
+// before it (base) and of it (sum), and over the whole list the survivors' (key >=
+// tau, a prefix) count and mass.  One barrier; it also sets S.ibin and S.flag to -1
+// for the sorted_find calls that follow.
+struct SortedScan {
+    int lo, hi;
+    u128 base, sum;
+    u128 Sv;
+    int ns;
+};
+
+FIE_DEV SortedScan sorted_scan(FinSmem& S, int nv, uint32_t tau)
 {
-    if (threadIdx.x == 0) S.flag = 0;
-    __syncthreads();
-    for (int i = threadIdx.x; i < n; i += kFinThreads) {
-        const uint32_t k = comp_k(S.cand[i]);
-        const bool in = strict ? k > t : k >= t;
-        const bool next_in = i + 1 < n && (strict ? comp_k(S.cand[i + 1]) > t : comp_k(S.cand[i + 1]) >= t);
-        if (in && !next_in) S.flag = i + 1;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int E = (nv + kFinThreads - 1) / kFinThreads;
+    SortedScan r;
+    r.lo = min(tid * E, nv);
+    r.hi = min(r.lo + E, nv);
+    u128 sum = 0, vsum = 0;
+    uint32_t vcnt = 0;
+    for (int i = r.lo; i < r.hi; ++i) {
+        const uint64_t c = S.cand[i];
+        const u128 w = comp_weight(S, c);
+        sum += w;
+        if (comp_k(c) >= tau) {
+            vsum += w;
+            ++vcnt;
+        }
+    }
+    const u128 incl = wave_incl_scan_u128(sum);
+    if (tau != 0) {                                   // uniform; tau == 0: every candidate survives
+        const u128 vw = wave_sum_u128(vsum);
+        const uint32_t vc = wave_sum_u32(vcnt);
+        if (lane == 63) {
+            S.red128[kFinWaves + wave] = vw;
+            S.red32[wave] = vc;
+        }
+    }
+    if (lane == 63) S.red128[wave] = incl;
+    if (tid == 0) {
+        S.ibin = -1;
+        S.flag = -1;
     }
     __syncthreads();
-    const int r = S.flag;
-    __syncthreads();
+    u128 before = 0, sv = 0;
+    uint32_t ns = 0;
+    for (int w = 0; w < kFinWaves; ++w) {
+        if (w < wave) before += S.red128[w];
+        if (tau != 0) {
+            sv += S.red128[kFinWaves + w];
+            ns += S.red32[w];
+        } else {
+            sv += S.red128[w];
+        }
+    }
+    if (tau == 0) ns = (uint32_t)nv;
+    r.base = before + incl - sum;
+    r.sum = sum;
+    r.Sv = sv;
+    r.ns = (int)ns;
     return r;
 }
 
-// Prefix masses (rule R1 weights) over the first m sorted candidates: thread t owns
-// the chunk [lo, hi) and knows the mass before it (base) and of it (sum).
-struct Chunks {
-    int lo, hi;
-    u128 base, sum;
-};
-
-FIE_DEV Chunks chunk_masses(FinSmem& S, int m)
+// The first sorted candidate whose inclusive prefix mass exceeds g, published by
+// the thread whose chunk holds it into *slot_i (left at -1 when none does) and its
+// prefix into *slot_m; read them after a barrier.
+FIE_DEV void sorted_find(FinSmem& S, const SortedScan& sc, u128 g, int* slot_i, u128* slot_m)
 {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int E = (m + kFinThreads - 1) / kFinThreads;
-    Chunks ch;
-    ch.lo = min(tid * E, m);
-    ch.hi = min(ch.lo + E, m);
-    ch.sum = 0;
-    for (int i = ch.lo; i < ch.hi; ++i) ch.sum += comp_weight(S, S.cand[i]);
-    const u128 incl = wave_incl_scan_u128(ch.sum);
-    if (lane == 63) S.red128[wave] = incl;
-    __syncthreads();
-    u128 before = 0;
-    for (int w = 0; w < wave; ++w) before += S.red128[w];
-    ch.base = before + incl - ch.sum;
-    __syncthreads();
-    return ch;
-}
-
-// The first sorted candidate i < lim whose inclusive prefix mass exceeds g, with
-// that prefix in *incl; -1 when the mass of the first lim candidates is <= g.
-FIE_DEV int chunk_find(FinSmem& S, const Chunks& ch, u128 g, int lim, u128* incl)
-{
-    if (threadIdx.x == 0) S.ibin = -1;
-    __syncthreads();
-    if (ch.lo < ch.hi && ch.base <= g && g < ch.base + ch.sum) {
-        u128 run = ch.base;
-        for (int i = ch.lo; i < ch.hi; ++i) {
+    if (sc.lo < sc.hi && sc.base <= g && g < sc.base + sc.sum) {
+        u128 run = sc.base;
+        for (int i = sc.lo; i < sc.hi; ++i) {
             run += comp_weight(S, S.cand[i]);
             if (run > g) {
-                S.ibin = i;
-                S.bex = run;
+                *slot_i = i;
+                *slot_m = run;
                 break;
             }
         }
     }
-    __syncthreads();
-    const int i = S.ibin;
-    *incl = S.bex;
-    __syncthreads();
-    return i >= 0 && i < lim ? i : -1;
-}
-
-// Mass of the first m sorted candidates (m <= the chunked length).
-FIE_DEV u128 chunk_prefix(FinSmem& S, const Chunks& ch, int m)
-{
-    if (threadIdx.x == 0) S.bme = 0;
-    __syncthreads();
-    if (m > 0 && ch.lo <= m - 1 && m - 1 < ch.hi) {
-        u128 run = ch.base;
-        for (int i = ch.lo; i < m; ++i) run += comp_weight(S, S.cand[i]);
-        S.bme = run;
-    }
-    __syncthreads();
-    const u128 r = S.bme;
-    __syncthreads();
-    return r;
 }
 
 // ---------------------------------------------------------------- k_finish, k_deep
@@ -1034,7 +1198,7 @@ FIE_DEV u128 chunk_prefix(FinSmem& S, const Chunks& ch, int m)
 // row: the full-row draw, and top-L logprobs deeper than the candidates.  Both
 // phases compute the same prologue (row maximum, tile table, row mass) from the
 // partials; a queued row's DeferRec carries what PH 1 cannot recompute cheaply.
-template <int DT, bool VEC, int PH>
+template <int DT, bool VEC, int PH, int Q>
 FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
 {
     const fie_sampler_args& a = P.a;
@@ -1057,58 +1221,131 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
 
     FIE_MARK(0);
     // Every per-tile partial this row reads, loaded together up front: the tile
-    // maxima, sums, candidate counts and bounds, and token 0's logit.
+    // maxima, sums, candidate counts and bounds, token 0's logit and count, and in
+    // PH 0 the candidate slots of the first kFinWaves * Q tiles (a tile's count
+    // arrives with them, so all its slots are read and the invalid ones dropped).
     const bool need_cand = !greedy || lp > 0;
+    const int lane = tid & 63, wave = tid >> 6;
     const size_t tbase = (size_t)row * NT + tid;
     const uint64_t pf_max = tid < NT ? P.w.maxc[tbase] : 0ull;
     const uint64_t pf_sw = (need_mass && tid < NT) ? P.w.sw[tbase] : 0ull;
     const uint32_t pf_nc = (need_cand && tid < NT) ? P.w.ncand[tbase] : 0u;
     const uint32_t pf_bd = (need_cand && tid < NT) ? P.w.bound[tbase] : 0u;
     const float x0 = P.w.tok0x[row];
-    // Tile maxima (x keys) and the row maximum.
-    if (tid < NT) S.tmc[tid] = pf_max;
+    const uint32_t c0 = pen ? P.w.tok0c[row] : 0u;
+    const bool spec = PH == 0 && need_cand;
+    // rows narrowed by mass (no top-k, no min-p) bin their candidates as they are taken
+    const bool bins = spec && !greedy && topk == 0 && !(mp > 0.0f);
+    if (bins) {
+        for (int i = tid; i < kPassBins; i += kFinThreads) {
+            S.pc[i] = 0;
+            S.pmf[i] = 0.0f;
+        }
+    }
+    uint64_t xs[Q + 1];
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        const int t = wave + kFinWaves * q;
+        xs[q] = spec && t < NT ? P.w.cand[((size_t)row * NT + t) * kCapW + lane] : 0ull;
+    }
+    // Round 1: the row maximum, the safety bound and the candidate count, per wave.
+    {
+        const uint64_t wm = wave_max_u64(pf_max);
+        const uint32_t wb = wave_max_u32(pf_bd);
+        const uint32_t wn = wave_sum_u32(pf_nc);
+        if (tid < NT) S.nc[tid] = pf_nc;
+        if (lane == 0) {
+            S.red64[wave] = wm;
+            S.red64[kFinWaves + wave] = ((uint64_t)wb << 32) | wn;
+        }
+        if (tid == 0) {
+            S.n = 0;
+            S.cmax = 0;
+        }
+    }
     __syncthreads();
-    const uint64_t xm = block_max_u64<kFinThreads>(tid < NT ? S.tmc[tid] : 0ull, S.red64);
+    uint64_t xm = 0;
+    uint32_t kx = 0, ncall = 0;
+    for (int w = 0; w < kFinWaves; ++w) {
+        xm = S.red64[w] > xm ? S.red64[w] : xm;
+        const uint64_t bn = S.red64[kFinWaves + w];
+        kx = (uint32_t)(bn >> 32) > kx ? (uint32_t)(bn >> 32) : kx;
+        ncall += (uint32_t)bn;
+    }
 
     FIE_MARK(1);
     // Token 0 (a tile of its own).
-    const uint32_t c0 = pen ? P.w.tok0c[row] : 0u;
     float w0 = x0;
     if (c0 && q1_keeps(S, P, row)) w0 = penalize(x0, rep, pres, freq, c0);
     const float y0 = s == 1.0f ? w0 + 0.0f : scaled(w0, s);
     const uint32_t k0 = fkey(y0);
 
-    // Row maximum M of y and the tile table of rule R1.
+    // Row maximum M of y and the tile table of rule R1: thread t for tile t (slot
+    // t + 1), the last thread for token 0 (slot 0); each slot's share of the row
+    // mass (rule R1: C_t times the tile sum of weights) summed per wave.
     const uint32_t kxm = xm ? fkey(y_of_xkey(comp_k(xm), s)) : 0u;
     const uint32_t Mkey = kxm > k0 ? kxm : k0;
     const float M = key_to_float(Mkey);
-    if (tid <= NT) {
-        float mt;
-        uint64_t ct;
-        if (tid == 0) {
-            mt = y0;
-            ct = fixed40(cexp(y0 - M));
-        } else {
-            const uint64_t c = S.tmc[tid - 1];
-            mt = c ? y_of_xkey(comp_k(c), s) : 0.0f;
-            ct = c ? fixed40(cexp(mt - M)) : 0ull;
+    {
+        u128 part = 0;
+        const bool z = tid == kFinThreads - 1;
+        if (tid < NT || z) {
+            float mt;
+            uint64_t ct;
+            if (z) {
+                mt = y0;
+                ct = fixed40(cexp(y0 - M));
+            } else {
+                mt = pf_max ? y_of_xkey(comp_k(pf_max), s) : 0.0f;
+                ct = pf_max ? fixed40(cexp(mt - M)) : 0ull;
+            }
+            const int slot = z ? 0 : tid + 1;
+            S.mt[slot] = mt;
+            S.ct[slot] = ct;
+            P.w.mt[(size_t)row * (NT + 1) + slot] = mt;
+            P.w.ct[(size_t)row * (NT + 1) + slot] = ct;
+            if (need_mass) part = z ? (u128)tok_weight(y0, y0) * ct : (u128)ct * pf_sw;
         }
-        S.mt[tid] = mt;
-        S.ct[tid] = ct;
-        P.w.mt[(size_t)row * (NT + 1) + tid] = mt;
-        P.w.ct[(size_t)row * (NT + 1) + tid] = ct;
+        if (need_mass) {
+            part = wave_sum_u128(part);
+            if (lane == 0) S.red128[wave] = part;
+        }
     }
-    __syncthreads();
+
+    // The safety key: every token whose scaled key exceeds it is a candidate.
+    uint32_t safe = 0;
+    if (kx <= 1u || kx <= kKeyNegInf) safe = 0;
+    else if (kx > kKeyPosInf) safe = 0xFFFFFFFFu;
+    else safe = fkey(y_of_xkey(kx, s));
 
     FIE_MARK(2);
-    // Whole-row mass (rule R1): sum over tiles of C_t * (tile sum of weights).
-    u128 sall = 0;
-    if (need_mass) {
-        u128 part = 0;
-        if (tid < NT) part = (u128)S.ct[tid + 1] * pf_sw;
-        if (tid == 0) part += (u128)tok_weight(y0, y0) * S.ct[0];
-        sall = block_sum_u128<kFinThreads>(part, S.red128);
+    // PH 0: the candidates as y-domain composites, those above the safety key into
+    // S.cand (binned when narrowed by mass); tiles past the held ones load now.
+    if (spec) {
+        uint64_t best = 0;
+        {
+            bool ok[Q + 1];
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const int t = wave + kFinWaves * q;
+                ok[q] = t < NT && (uint32_t)lane < S.nc[t];
+                xs[q] = ok[q] ? cand_y(xs[q], s) : 0ull;
+            }
+            ok[Q] = tid == kFinThreads - 1;
+            xs[Q] = comp_key(k0, 0);
+            FIE_MARK(15);
+            cand_commit(S, xs, ok, safe, best, bins, M);
+        }
+        for (int t0 = kFinWaves * Q; t0 < NT; t0 += kFinWaves * Q)
+            cand_batch<Q>(S, P, row, NT, t0, s, safe, best, bins, M, false, 0ull);
+        best = wave_max_u64(best);
+        if (lane == 0 && best) atomicMax((unsigned long long*)&S.cmax, (unsigned long long)best);
     }
+    // Round 2: the row mass and the candidates.
+    __syncthreads();
+    u128 sall = 0;
+    if (need_mass)
+        for (int w = 0; w < kFinWaves; ++w) sall += S.red128[w];
 
     FIE_MARK(3);
     int64_t token = -1;
@@ -1146,37 +1383,20 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
         T = comp_weight(S, best);
     }
 
-    // Candidates as y-domain composites, sorted, and the safety key: every token
-    // whose scaled key exceeds `safe` is among them.
-    int n = 0, nv = 0;       // candidates, and those above the safety key (sorted)
+    // Candidates as y-domain composites, sorted: every token whose scaled key
+    // exceeds `safe` is among them.
+    int n = need_cand ? (int)ncall + 1 : 0;   // candidates, token 0 included
+    int nv = 0;              // those above the safety key (sorted)
     int nvall = 0;           // nv before narrowing to a prefix
-    uint32_t safe = 0;
     uint64_t cmax = 0;       // the largest candidate composite
     bool sorted = false;
     if (need_cand) {
-        // per-tile counts and bounds: one load per thread, a block prefix sum
-        const uint32_t m = pf_nc;
-        const uint32_t b = pf_bd;
-        uint32_t total;
-        const uint32_t off = block_excl_scan_u32<kFinThreads>(m, S.red32, &total);
-        if (tid < NT) S.coff[tid] = off;
-        const uint32_t kxm = block_max_u32<kFinThreads>(b, S.red32);
-        if (tid == 0) { S.coff[NT] = total; S.n = total + 1; S.red32[16] = kxm; }
-        __syncthreads();
-        n = (int)S.n;
-        const uint32_t kx = S.red32[16];
-        __syncthreads();
-        if (kx <= 1u || kx <= kKeyNegInf) safe = 0;
-        else if (kx > kKeyPosInf) safe = 0xFFFFFFFFu;
-        else safe = fkey(y_of_xkey(kx, s));
-        // only the complete region is ever used: candidates at or below the safety
-        // key are dropped before sorting (S.cmax keeps the largest of all)
         FIE_MARK(12);
         if (PH == 1) {
             // the row was queued: its candidates are reloaded below only for logprobs
             deep = dr.mode == kDeferDraw;
         } else {
-        nv = load_candidates(S, P, row, NT, n, s, k0, safe);
+        nv = (int)S.n;
         cmax = S.cmax;
         FIE_MARK(13);
         FIE_WHY(0, (uint32_t)nv);
@@ -1200,7 +1420,9 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
                 if (by_mass && sall == 0) narrow = false;
             }
             nvall = nv;
-            if (narrow && (cnt > 0 || by_mass)) nv = narrow_candidates(S, nv, M, cnt, by_mass, g);
+            if (narrow && (cnt > 0 || by_mass))
+                nv = by_mass ? narrow_binned(S, nv, M, cnt, g) : narrow_candidates(S, nv, M, cnt, false, g);
+            FIE_WHY(2, (uint32_t)nv);
             FIE_MARK(14);
             sort_desc(S, nv);
             sorted = true;
@@ -1237,18 +1459,19 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
             if (!deep) {
                 // survivors (key >= tau) and the complete region (key > safe) are
                 // prefixes of the sorted candidates; with tau != 0 the survivors lie in it
-                const int ns = tau != 0 ? sorted_prefix(S, nv, tau, false) : nv;
-                const Chunks ch = chunk_masses(S, nv);
-                const u128 Sv = tau != 0 ? chunk_prefix(S, ch, ns) : sall;
+                const SortedScan sc = sorted_scan(S, nv, tau);
+                const int ns = tau != 0 ? sc.ns : nv;
+                const u128 Sv = tau != 0 ? sc.Sv : sall;
                 FIE_MARK(6);
                 int lim = ns;
                 cut = 0;
                 if (tp < 1.0f) {
                     const u128 thr = ceil_mul_f32(tp, Sv);
-                    u128 incl;
-                    const int i = chunk_find(S, ch, thr - 1, lim, &incl);
-                    if (i < 0) { (partial ? miss : deep) = true; FIE_WHY(2, 100 + (uint32_t)partial); FIE_WHY(3, (uint32_t)nv); }
-                    else { cut = S.cand[i]; T = incl; lim = i + 1; }
+                    sorted_find(S, sc, thr - 1, &S.ibin, &S.bex);
+                    __syncthreads();
+                    const int i = S.ibin;
+                    if (i < 0 || i >= lim) { (partial ? miss : deep) = true; FIE_WHY(2, 100 + (uint32_t)partial); FIE_WHY(3, (uint32_t)nv); }
+                    else { cut = S.cand[i]; T = S.bex; lim = i + 1; }
                 } else {
                     T = Sv;
                 }
@@ -1259,9 +1482,10 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
                         tok_comp = cmax;
                     } else {
                         const u128 g = floor_mul_f64(urow, T);
-                        u128 incl;
-                        const int i = chunk_find(S, ch, g, lim, &incl);
-                        if (i < 0) { (partial ? miss : deep) = true; FIE_WHY(2, 200 + (uint32_t)partial); FIE_WHY(3, (uint32_t)nv); }
+                        sorted_find(S, sc, g, &S.flag, &S.bme);
+                        __syncthreads();
+                        const int i = S.flag;
+                        if (i < 0 || i >= lim) { (partial ? miss : deep) = true; FIE_WHY(2, 200 + (uint32_t)partial); FIE_WHY(3, (uint32_t)nv); }
                         else { token = comp_idx(S.cand[i]); tok_comp = S.cand[i]; }
                     }
                 }
@@ -1269,7 +1493,7 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
             FIE_MARK(8);
             if (!deep && !miss && a.tk_key && tid == 0) a.tk_key[row] = tk;
             if (!miss) break;
-            nv = load_candidates(S, P, row, NT, n, s, k0, safe);
+            nv = load_candidates(S, P, row, NT, s, k0, safe);
             nvall = nv;
             sort_desc(S, nv);
         }
@@ -1331,7 +1555,7 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
         // the LDS candidates were overwritten: reload them for the logprobs below
         sorted = false;
         if (lp > 0 && n > 0) {
-            nv = load_candidates(S, P, row, NT, n, s, k0, safe);
+            nv = load_candidates(S, P, row, NT, s, k0, safe);
             if (nv <= kSortMax) {
                 sort_desc(S, nv);
                 sorted = true;
@@ -1415,15 +1639,20 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
     }
 }
 
-template <int DT, bool VEC>
-__global__ __launch_bounds__(kFinThreads, 4) void k_finish(const KParams P)
+// One workgroup per row.  A row's finish is a chain of dependent steps, so its
+// latency is the kernel's: with no more rows than CUs (one workgroup each) the WIDE
+// variant takes up to 256 registers a lane and spills nothing; larger batches take
+// 128 (two workgroups a CU).
+template <int DT, bool VEC, bool WIDE>
+__global__ __launch_bounds__(kFinThreads, WIDE ? 2 : 4) void k_finish(const KParams P)
 {
     __shared__ FinSmem S;
-    finish_row<DT, VEC, 0>(S, P, blockIdx.x);
+    finish_row<DT, VEC, 0, WIDE ? 10 : kReloadQ>(S, P, blockIdx.x);
 }
 
 // A fixed grid taking queued rows one at a time; every workgroup leaves once the
-// queue is drained (the count is final: k_finish has completed).
+// queue is drained (the count is final: k_finish has completed).  The queue is
+// short in decode (a few rows a step) but holds every row of a flat batch.
 template <int DT, bool VEC>
 __global__ __launch_bounds__(kFinThreads, 4) void k_deep(const KParams P)
 {
@@ -1431,7 +1660,7 @@ __global__ __launch_bounds__(kFinThreads, 4) void k_deep(const KParams P)
     const uint32_t queued = P.w.dq[0];
     const uint32_t total = queued < (uint32_t)P.a.rows ? queued : (uint32_t)P.a.rows;
     if (blockIdx.x >= total) return;
-    finish_row<DT, VEC, 1>(S, P, (int)P.w.dqrows[blockIdx.x]);
+    finish_row<DT, VEC, 1, kReloadQ>(S, P, (int)P.w.dqrows[blockIdx.x]);
 }
 
 }  // namespace fie

@@ -276,6 +276,21 @@ static int launch_scan(const KParams& P, bool vec, bool longh, hipStream_t st)
     return FIE_OK;
 }
 
+// Compute units of the current device (queried once per device; 0 when unknown,
+// which selects the narrow k_finish).
+static int cu_count()
+{
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (cus[dev] == 0) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = -1;
+        cus[dev] = n;
+    }
+    return cus[dev] > 0 ? cus[dev] : 0;
+}
+
 template <int DT>
 static int launch_finish(const KParams& P, bool vec, bool deep, hipStream_t st)
 {
@@ -286,8 +301,14 @@ static int launch_finish(const KParams& P, bool vec, bool deep, hipStream_t st)
         FIE_LAUNCH_CHECK("k_deep");
         return FIE_OK;
     }
-    if (vec) k_finish<DT, true><<<P.a.rows, kFinThreads, 0, st>>>(P);
-    else k_finish<DT, false><<<P.a.rows, kFinThreads, 0, st>>>(P);
+    const bool wide = P.a.rows <= cu_count();
+    if (vec) {
+        if (wide) k_finish<DT, true, true><<<P.a.rows, kFinThreads, 0, st>>>(P);
+        else k_finish<DT, true, false><<<P.a.rows, kFinThreads, 0, st>>>(P);
+    } else {
+        if (wide) k_finish<DT, false, true><<<P.a.rows, kFinThreads, 0, st>>>(P);
+        else k_finish<DT, false, false><<<P.a.rows, kFinThreads, 0, st>>>(P);
+    }
     FIE_LAUNCH_CHECK("k_finish");
     return FIE_OK;
 }

@@ -112,6 +112,23 @@ def test_c4_full_batch_properties(fs):
     np.testing.assert_array_equal(out["cut_comp"][rows], ref.cut_comp)
 
 
+def test_finish_register_variants_agree(fs):
+    """A batch with more rows than the GPU has CUs takes the 128-register k_finish; C3's
+    256 rows take the wide one.  The same rows in both (C3 plus every fourth row again,
+    320 in all) give identical tokens, cuts, thresholds and kept masses."""
+    w = W.make(3)
+    V = w.logits.shape[1]
+    extra = list(range(0, 256, 4))
+    idx = list(range(256)) + extra
+    print(f"  case: C3 rows 0..255 + {len(extra)} repeats, vocab={V}", flush=True)
+    big, _, _ = fs.step(w.logits[idx].to(DEV), resolve_params(
+        [w.params[i] for i in idx], V, w.uniforms[idx], [w.contexts[i] for i in idx]))
+    small, _, _ = fs.step(w.logits.to(DEV), resolve_params(w.params, V, w.uniforms, w.contexts))
+    for key in ("tokens", "cut_comp", "tk_key", "kept_mass"):
+        np.testing.assert_array_equal(big[key][:256], small[key], err_msg=key)
+        np.testing.assert_array_equal(big[key][256:], small[key][extra], err_msg=key)
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
 def test_argmax_first_index_on_ties(fs, dtype):
     g = torch.Generator().manual_seed(7)
