@@ -68,6 +68,8 @@ struct FinSmem {
     uint32_t bcnt;
     uint64_t cmax;
     SelResult sel;
+    DeferRec dfr;                               // a row deferred to the full-row path in place
+    uint32_t dmode;                             // its mode (0: not deferred)
 };
 
 // Weight of a y-domain composite under rule R1: floor(cexp(y - m_t) 2^40) * C_t.
@@ -1199,7 +1201,7 @@ FIE_DEV void sorted_find(FinSmem& S, const SortedScan& sc, u128 g, int* slot_i, 
 // phases compute the same prologue (row maximum, tile table, row mass) from the
 // partials; a queued row's DeferRec carries what PH 1 cannot recompute cheaply.
 template <int DT, bool VEC, int PH, int Q>
-FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
+FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool inl)
 {
     const fie_sampler_args& a = P.a;
     const int tid = threadIdx.x, NT = P.NT;
@@ -1261,6 +1263,7 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
         if (tid == 0) {
             S.n = 0;
             S.cmax = 0;
+            if (PH == 0) S.dmode = 0;            // PH 1 in place: the caller has read it
         }
     }
     __syncthreads();
@@ -1356,8 +1359,9 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
     bool deep = false;
     double lse = 0.0;
     DeferRec dr{};
-    if (PH == 1) dr = P.w.dfr[row];
-    // PH 0: hand the row to k_deep with what is settled so far
+    if (PH == 1) dr = inl ? S.dfr : P.w.dfr[row];
+    // PH 0: hand the row to the full-row path with what is settled so far: in place
+    // (inl: the caller runs PH 1 next, the record in LDS) or queued for k_deep
     auto defer = [&](uint32_t mode) {
         if (tid == 0) {
             DeferRec d;
@@ -1368,9 +1372,14 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row)
             d.token = token;
             d.tau = tau;
             d.mode = mode;
-            P.w.dfr[row] = d;
-            const uint32_t at = atomicAdd(&P.w.dq[0], 1u);
-            if (at < (uint32_t)a.rows) P.w.dqrows[at] = (uint32_t)row;
+            S.dmode = mode;
+            if (inl) {
+                S.dfr = d;
+            } else {
+                P.w.dfr[row] = d;
+                const uint32_t at = atomicAdd(&P.w.dq[0], 1u);
+                if (at < (uint32_t)a.rows) P.w.dqrows[at] = (uint32_t)row;
+            }
         }
     };
     if (lp >= 0) lse = log(u128_to_double(sall)) - 80.0 * 0.69314718055994530942;
@@ -1647,7 +1656,12 @@ template <int DT, bool VEC, bool WIDE>
 __global__ __launch_bounds__(kFinThreads, WIDE ? 2 : 4) void k_finish(const KParams P)
 {
     __shared__ FinSmem S;
-    finish_row<DT, VEC, 0, WIDE ? 10 : kReloadQ>(S, P, blockIdx.x);
+    finish_row<DT, VEC, 0, WIDE ? 10 : kReloadQ>(S, P, blockIdx.x, WIDE);
+    if constexpr (WIDE) {
+        // a row the candidates could not settle takes the full-row path here, at once
+        __syncthreads();
+        if (S.dmode) finish_row<DT, VEC, 1, kReloadQ>(S, P, blockIdx.x, true);
+    }
 }
 
 // A fixed grid taking queued rows one at a time; every workgroup leaves once the
@@ -1660,7 +1674,7 @@ __global__ __launch_bounds__(kFinThreads, 4) void k_deep(const KParams P)
     const uint32_t queued = P.w.dq[0];
     const uint32_t total = queued < (uint32_t)P.a.rows ? queued : (uint32_t)P.a.rows;
     if (blockIdx.x >= total) return;
-    finish_row<DT, VEC, 1, kReloadQ>(S, P, (int)P.w.dqrows[blockIdx.x]);
+    finish_row<DT, VEC, 1, kReloadQ>(S, P, (int)P.w.dqrows[blockIdx.x], false);
 }
 
 }  // namespace fie

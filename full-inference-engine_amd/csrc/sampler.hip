@@ -291,6 +291,10 @@ static int cu_count()
     return cus[dev] > 0 ? cus[dev] : 0;
 }
 
+// With no more rows than CUs, k_finish runs the wide variant, which takes a row its
+// candidates cannot settle through the full-row path itself: k_deep has no queue.
+static bool finish_in_place(const KParams& P) { return P.a.rows <= cu_count(); }
+
 template <int DT>
 static int launch_finish(const KParams& P, bool vec, bool deep, hipStream_t st)
 {
@@ -301,7 +305,7 @@ static int launch_finish(const KParams& P, bool vec, bool deep, hipStream_t st)
         FIE_LAUNCH_CHECK("k_deep");
         return FIE_OK;
     }
-    const bool wide = P.a.rows <= cu_count();
+    const bool wide = finish_in_place(P);
     if (vec) {
         if (wide) k_finish<DT, true, true><<<P.a.rows, kFinThreads, 0, st>>>(P);
         else k_finish<DT, true, false><<<P.a.rows, kFinThreads, 0, st>>>(P);
@@ -421,7 +425,7 @@ int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, vo
     rc = run_stage(P, FIE_STAGE_SCAN, st);
     if (rc != FIE_OK) return rc;
     rc = run_stage(P, FIE_STAGE_FINISH, st);
-    if (rc != FIE_OK) return rc;
+    if (rc != FIE_OK || finish_in_place(P)) return rc;
     return run_stage(P, FIE_STAGE_DEEP, st);
 }
 
@@ -450,7 +454,7 @@ static int lmhead_run(const fie_sampler_args* args, const void* hidden, const vo
                                 : launch_lmhead<FIE_BF16>(P, hidden, weight, hidden_dim, vec, longh, st);
     if (rc != FIE_OK || !whole) return rc;
     rc = run_stage(P, FIE_STAGE_FINISH, st);
-    if (rc != FIE_OK) return rc;
+    if (rc != FIE_OK || finish_in_place(P)) return rc;
     return run_stage(P, FIE_STAGE_DEEP, st);
 }
 

@@ -136,9 +136,11 @@ typedef struct fie_workspace {
    most `vocab` (0 on invalid sizes). */
 size_t fie_sampler_workspace_size(int32_t max_rows, int32_t vocab);
 
-/* One sampler step: sampler.py:81-117 minus host bookkeeping.  Four kernels: the
-   penalty histories bucketed by span, one streaming read of the logits, one
-   workgroup per row, then the rows the candidates could not settle. */
+/* One sampler step: sampler.py:81-117 minus host bookkeeping.  Up to four kernels:
+   the penalty histories bucketed by span, one streaming read of the logits, one
+   workgroup per row, then the rows the candidates could not settle (with no more
+   rows than the GPU has CUs, the per-row kernel settles those itself and the fourth
+   is not launched). */
 int fie_sampler_sample(const fie_sampler_args* args, const fie_workspace* ws, void* stream);
 
 /* fie_sampler_sample with the model's output projection fused in front of it.  The
@@ -169,7 +171,8 @@ enum {
     FIE_STAGE_PREP = 0,        /* the penalty histories bucketed by span (no-op without penalties) */
     FIE_STAGE_SCAN = 1,        /* the streaming pass over the logits */
     FIE_STAGE_FINISH = 2,      /* the per-row selection and draw from the candidates */
-    FIE_STAGE_DEEP = 3,        /* the rows FINISH queued: passes over the whole row (no-op when none) */
+    FIE_STAGE_DEEP = 3,        /* the rows FINISH queued: passes over the whole row (no-op when none;
+                                  FINISH queues none when rows <= the GPU's CUs) */
 };
 int fie_sampler_stage(const fie_sampler_args* args, const fie_workspace* ws, int32_t stage,
                       void* stream);
