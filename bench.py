@@ -2,8 +2,9 @@
 
 One step = one fused sampler call (penalties, temperature, top-k / top-p / min-p,
 draw, logprobs) over one [B, V] logits batch already resident in HBM, with the
-step's parameters and penalty histories resident too: the four kernels k_prep,
-k_scan, k_finish and k_deep (idle when no row needs the full-row path).  Logits rotate through enough distinct buffers (> 512 MB) that the 256 MB
+step's parameters and penalty histories resident too: the kernels k_prep, k_scan,
+k_finish and, for batches with more rows than CUs, k_deep (idle when no row needs
+the full-row path).  Logits rotate through enough distinct buffers (> 512 MB) that the 256 MB
 Infinity Cache cannot serve them.
 
 Prints one JSON line: rows/s and us/step for the headline config, the roofline of
@@ -143,6 +144,8 @@ def time_config(config: int, steps: int, warmup: int, ring_mb: int, dev):
         stage_ms.append(e0.elapsed_time(e1) / steps)
     if not hp.apply_penalties:
         stage_ms[0] = 0.0                                   # k_prep is not launched
+    if B <= torch.cuda.get_device_properties(dev).multi_processor_count:
+        stage_ms[3] = 0.0                                   # k_finish settles every row: no k_deep
 
     # One checked step: status bits of the rows (the exact path is informational).
     buf.download(stream)
