@@ -214,6 +214,36 @@ def test_exact_path_rows(fs):
     check(out, ref, params, gk, gp, lp=True)
 
 
+def test_queued_full_row_path_matches_in_place(fs):
+    """Rows outside the candidates go through the full-row path inside k_finish when a
+    batch fits the CUs, and through k_deep's queue when it does not: the eight rows
+    above, alone and repeated 33 times (264 rows), give identical outputs."""
+    rng = np.random.default_rng(5)
+    rows, vocab = 8, 151936
+    x = torch.from_numpy(rng.normal(0, 0.2, (rows, vocab)).astype(np.float32)).to(torch.bfloat16)
+    params = [SamplingParams(temperature=1.0, top_k=5000),
+              SamplingParams(temperature=1.0, top_p=0.99),
+              SamplingParams(temperature=1.0),
+              SamplingParams(temperature=1.0, min_p=0.5, logprobs=20),
+              SamplingParams(temperature=0.9, top_k=3000, top_p=0.97, logprobs=3),
+              SamplingParams(temperature=1.7, top_p=0.999),
+              SamplingParams(logprobs=5),
+              SamplingParams(temperature=1.0, top_k=100000, top_p=0.5)]
+    u = rng.random(rows)
+    rep = 33
+    print(f"  case: 8 full-row rows alone and x{rep}, vocab={vocab}", flush=True)
+    one, _, _ = fs.step(x.to(DEV), resolve_params(params, vocab, u, None))
+    many, _, _ = fs.step(x.repeat(rep, 1).to(DEV), resolve_params(params * rep, vocab, np.tile(u, rep), None))
+    assert (many["status"] & _lib.FIE_ROW_EXACT_PATH).any()
+    for key in ("status", "tokens", "tk_key", "cut_comp", "kept_mass", "row_mass"):
+        want = np.concatenate([one[key]] * rep)
+        np.testing.assert_array_equal(many[key], want, err_msg=key)
+    lp_rows = [i for i, p in enumerate(params) if p.logprobs is not None]   # others write no logprobs
+    for key in ("chosen_lp", "top_ids", "top_lp"):
+        for r in range(rep):
+            np.testing.assert_array_equal(many[key][[r * rows + i for i in lp_rows]], one[key][lp_rows], err_msg=key)
+
+
 def test_ties_and_constant_rows(fs):
     rows, vocab = 6, 40000
     x = torch.zeros(rows, vocab)
