@@ -13,15 +13,6 @@
 
 namespace fie {
 
-#ifdef FIE_PHASE_PROFILE
-__device__ uint64_t g_fie_prof[8192 * 16];
-#define FIE_MARK(i) do { if (threadIdx.x == 0 && row < 8192) g_fie_prof[(size_t)row * 16 + (i)] = __builtin_amdgcn_s_memtime(); } while (0)
-__device__ uint32_t g_fie_why[8192 * 4];
-#define FIE_WHY(k, v) do { if (threadIdx.x == 0 && row < 8192) g_fie_why[(size_t)row * 4 + (k)] = (v); } while (0)
-#else
-#define FIE_WHY(k, v) do { } while (0)
-#define FIE_MARK(i) do { } while (0)
-#endif
 
 constexpr int kFinThreads = 512;
 constexpr int kGCap = 4096;        // composites held in LDS (candidates / a gathered bin)
@@ -566,7 +557,6 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
         atomicAdd(&S.pc[b], 1u);
         bin_add(S, b, weight_of(S, y, idx));
     });
-    FIE_MARK(12);
     // S.cand holds the elements (ncur of them) of bins [cur_lo, cur_hi] and, when
     // cur2_lo >= 0, of bins [cur2_lo, cur2_hi] as well.
     int cur_lo = -1, cur_hi = -1, cur2_lo = -1, cur2_hi = -1, ncur = 0;
@@ -649,7 +639,6 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
                 dl = dh = -1;
                 if (!gather(b, b)) return false;
             }
-            FIE_MARK(13);
             // within bin b only: composites of the lower bins (the draw's run) are larger
             uint64_t chi = ~0ull;
             if (dl >= 0) {
@@ -671,7 +660,6 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
             T = above + r.excl + r.meas;
             bc = b;
             lastc = T - above;
-            FIE_MARK(14);
         }
     }
 
@@ -712,7 +700,6 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
         if (!r.found) return false;
         tok = r.comp;
     }
-    FIE_MARK(15);
     *tk_out = tk;
     *tau_out = tau;
     *cut_out = cut;
@@ -1221,7 +1208,6 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
     int32_t status = 0;
     if (pen && P.w.bad[row] && !a.hist_invalid) status |= FIE_ROW_UNCOUNTED_IDS;
 
-    FIE_MARK(0);
     // Every per-tile partial this row reads, loaded together up front: the tile
     // maxima, sums, candidate counts and bounds, token 0's logit and count, and in
     // PH 0 the candidate slots of the first kFinWaves * Q tiles (a tile's count
@@ -1276,7 +1262,6 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
         ncall += (uint32_t)bn;
     }
 
-    FIE_MARK(1);
     // Token 0 (a tile of its own).
     float w0 = x0;
     if (c0 && q1_keeps(S, P, row)) w0 = penalize(x0, rep, pres, freq, c0);
@@ -1321,7 +1306,6 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
     else if (kx > kKeyPosInf) safe = 0xFFFFFFFFu;
     else safe = fkey(y_of_xkey(kx, s));
 
-    FIE_MARK(2);
     // PH 0: the candidates as y-domain composites, those above the safety key into
     // S.cand (binned when narrowed by mass); tiles past the held ones load now.
     if (spec) {
@@ -1336,7 +1320,6 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
             }
             ok[Q] = tid == kFinThreads - 1;
             xs[Q] = comp_key(k0, 0);
-            FIE_MARK(15);
             cand_commit(S, xs, ok, safe, best, bins, M);
         }
         for (int t0 = kFinWaves * Q; t0 < NT; t0 += kFinWaves * Q)
@@ -1350,7 +1333,6 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
     if (need_mass)
         for (int w = 0; w < kFinWaves; ++w) sall += S.red128[w];
 
-    FIE_MARK(3);
     int64_t token = -1;
     uint64_t tok_comp = 0;   // y-domain composite of the chosen token
     uint32_t tau = 0;
@@ -1400,16 +1382,14 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
     uint64_t cmax = 0;       // the largest candidate composite
     bool sorted = false;
     if (need_cand) {
-        FIE_MARK(12);
         if (PH == 1) {
             // the row was queued: its candidates are reloaded below only for logprobs
             deep = dr.mode == kDeferDraw;
         } else {
         nv = (int)S.n;
         cmax = S.cmax;
-        FIE_MARK(13);
-        FIE_WHY(0, (uint32_t)nv);
-        FIE_WHY(1, (uint32_t)n);
+
+
         if (nv > kSortMax) {
             deep = true;
         } else {
@@ -1431,8 +1411,7 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
             nvall = nv;
             if (narrow && (cnt > 0 || by_mass))
                 nv = by_mass ? narrow_binned(S, nv, M, cnt, g) : narrow_candidates(S, nv, M, cnt, false, g);
-            FIE_WHY(2, (uint32_t)nv);
-            FIE_MARK(14);
+
             sort_desc(S, nv);
             sorted = true;
         }
@@ -1450,7 +1429,6 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
     // narrowed prefix holds every crossing by construction; should a cut or draw
     // still miss it, that is not a verdict: every candidate is then loaded and
     // sorted and the selection runs again.
-    FIE_MARK(4);
     if (PH == 0 && !greedy && !deep) {
         for (;;) {
             const bool partial = nv < nvall;
@@ -1464,14 +1442,12 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
             const uint32_t tmp = minp_key(M, mp);
             tau = tk > tmp ? tk : tmp;
             if (!deep && tau != 0 && tau <= safe) deep = true;
-            FIE_MARK(5);
             if (!deep) {
                 // survivors (key >= tau) and the complete region (key > safe) are
                 // prefixes of the sorted candidates; with tau != 0 the survivors lie in it
                 const SortedScan sc = sorted_scan(S, nv, tau);
                 const int ns = tau != 0 ? sc.ns : nv;
                 const u128 Sv = tau != 0 ? sc.Sv : sall;
-                FIE_MARK(6);
                 int lim = ns;
                 cut = 0;
                 if (tp < 1.0f) {
@@ -1479,12 +1455,11 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
                     sorted_find(S, sc, thr - 1, &S.ibin, &S.bex);
                     __syncthreads();
                     const int i = S.ibin;
-                    if (i < 0 || i >= lim) { (partial ? miss : deep) = true; FIE_WHY(2, 100 + (uint32_t)partial); FIE_WHY(3, (uint32_t)nv); }
+                    if (i < 0 || i >= lim) (partial ? miss : deep) = true;
                     else { cut = S.cand[i]; T = S.bex; lim = i + 1; }
                 } else {
                     T = Sv;
                 }
-                FIE_MARK(7);
                 if (!deep && !miss) {
                     if (T == 0) {
                         token = comp_idx(cmax);
@@ -1494,12 +1469,11 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
                         sorted_find(S, sc, g, &S.flag, &S.bme);
                         __syncthreads();
                         const int i = S.flag;
-                        if (i < 0 || i >= lim) { (partial ? miss : deep) = true; FIE_WHY(2, 200 + (uint32_t)partial); FIE_WHY(3, (uint32_t)nv); }
+                        if (i < 0 || i >= lim) (partial ? miss : deep) = true;
                         else { token = comp_idx(S.cand[i]); tok_comp = S.cand[i]; }
                     }
                 }
             }
-            FIE_MARK(8);
             if (!deep && !miss && a.tk_key && tid == 0) a.tk_key[row] = tk;
             if (!miss) break;
             nv = load_candidates(S, P, row, NT, s, k0, safe);
@@ -1508,7 +1482,6 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
         }
     }
 
-    FIE_MARK(9);
     // Full-row path for sampled rows the candidates could not settle.
     if (PH == 0 && !greedy && deep) {
         defer(kDeferDraw);
@@ -1572,7 +1545,6 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
         }
     }
 
-    FIE_MARK(10);
     // Logprobs (sampler.py:262-291, rule R7): chosen token, then the row's best L,
     // all from the penalised, scaled distribution before filtering.
     if (lp >= 0) {
@@ -1626,7 +1598,6 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
         }
     }
 
-    FIE_MARK(11);
     if (tid == 0) {
         a.tokens[row] = token;
         if (a.status) a.status[row] = status;

@@ -11,7 +11,7 @@
 // tile it produced: the tile partials k_scan would have read back from HBM.
 #pragma once
 
-#include "scan.h"
+#include "launchers.h"
 
 namespace fie {
 
@@ -21,7 +21,6 @@ constexpr int kLhWaves = kLhThreads / 64;
 constexpr int kLhSub = 128;                   // tokens per sub-block (64 per token group)
 constexpr int kLhK = 32;                      // K of one MFMA step
 constexpr int kLhKStage = 64;                 // K of one pipeline stage (two MFMA steps)
-constexpr int kLhKAlign = 128;                // the hidden size must be a multiple
 constexpr int kLhStages = 3;                  // LDS stages (two in flight while one is used)
 constexpr int kLhRowsPerWave = kLhRows / kLhWaves;
 // One stage in 16-byte chunks: A 64 rows x 8, then B 128 tokens x 8; three per thread.

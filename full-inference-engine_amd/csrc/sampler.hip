@@ -1,6 +1,6 @@
 // MI355X fused token sampler: kernels behind the C ABI of include/fie_sampler.h.
 //
-//   k_prep      penalty histories bucketed by span                (scan.h)
+//   k_prep      penalty histories bucketed by span                (here)
 //   k_scan      one streaming read of the logits, tile partials   (scan.h)
 //   k_finish    one workgroup per row: exact selection and draw   (finish.h)
 //   k_argmax_*  the greedy fast path, logits.argmax(-1)           (sampler.py:106)
@@ -15,11 +15,61 @@
 
 #include <mutex>
 
-#include "finish.h"
-#include "lmhead.h"
+#include "launchers.h"
 #include "fie_sampler.h"
 
 namespace fie {
+
+// ---------------------------------------------------------------- k_prep
+// Buckets the history of every penalised row by span (sampler.py:134-144 counts
+// the same ids): the offsets inside the span of the first kBucketCap ids of each
+// span, the number of ids per span, the occurrences of token 0 and of ids >= vocab.
+// Each k_scan workgroup then reads its own span's bucket instead of the whole
+// history.  The order inside a bucket is free: only counts are taken from it.
+__global__ __launch_bounds__(kPrepThreads) void k_prep(const KParams P)
+{
+    __shared__ uint32_t sc[kMaxSpans];
+    __shared__ uint32_t zc, badc;
+    const fie_sampler_args& a = P.a;
+    const int row = blockIdx.x, tid = threadIdx.x, NS = P.NS;
+    const uint32_t V = (uint32_t)a.vocab;
+    // the row's flags and history range are loaded together (one round trip)
+    const int32_t fl = a.flags[row];
+    const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
+    if (!(a.apply_penalties && (fl & FIE_FLAG_PENALTY))) return;
+    if (tid < NS) sc[tid] = 0;
+    if (tid == 0) { zc = 0; badc = 0; }
+    __syncthreads();
+    uint16_t* bk = P.w.bk + (size_t)row * NS * kBucketCap;
+    constexpr int kPer = 8;   // ids per thread per batch, loaded together
+    for (int64_t base = h0; base < h1; base += (int64_t)kPer * kPrepThreads) {
+        uint32_t ids[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int64_t h = base + q * kPrepThreads + tid;
+            ids[q] = h < h1 ? (uint32_t)a.hist_ids[h] : 0xFFFFFFFFu;
+        }
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const uint32_t id = ids[q];
+            if (id == 0) {
+                atomicAdd(&zc, 1u);
+            } else if (id < V) {
+                const uint32_t sp = id / (uint32_t)kSpan;
+                const uint32_t at = atomicAdd(&sc[sp], 1u);
+                if (at < (uint32_t)kBucketCap) bk[sp * kBucketCap + at] = (uint16_t)(id % (uint32_t)kSpan);
+            } else if (base + q * kPrepThreads + tid < h1) {
+                atomicAdd(&badc, 1u);
+            }
+        }
+    }
+    __syncthreads();
+    if (tid < NS) P.w.nb[(size_t)row * NS + tid] = sc[tid];
+    if (tid == 0) {
+        P.w.tok0c[row] = zc;
+        P.w.bad[row] = badc;
+    }
+}
 
 // ---------------------------------------------------------------- greedy fast path
 constexpr int kArgChunk = 8192;   // tokens per workgroup of the argmax pass
@@ -261,19 +311,11 @@ static bool vec_ok(const void* p, int64_t stride, int sz)
         }                                                                               \
     } while (0)
 
-template <int DT>
-static int launch_scan(const KParams& P, bool vec, bool longh, hipStream_t st)
+static int launch_status(hipError_t e, const char* what)
 {
-    const dim3 grid(P.NS, P.a.rows);
-    if (vec) {
-        if (longh) k_scan<DT, true, true><<<grid, kScanThreads, 0, st>>>(P);
-        else k_scan<DT, true, false><<<grid, kScanThreads, 0, st>>>(P);
-    } else {
-        if (longh) k_scan<DT, false, true><<<grid, kScanThreads, 0, st>>>(P);
-        else k_scan<DT, false, false><<<grid, kScanThreads, 0, st>>>(P);
-    }
-    FIE_LAUNCH_CHECK("k_scan");
-    return FIE_OK;
+    if (e == hipSuccess) return FIE_OK;
+    snprintf(g_err, sizeof g_err, "%s: %s", what, hipGetErrorString(e));
+    return FIE_E_LAUNCH;
 }
 
 // Compute units of the current device (queried once per device; 0 when unknown,
@@ -295,28 +337,6 @@ static int cu_count()
 // candidates cannot settle through the full-row path itself: k_deep has no queue.
 static bool finish_in_place(const KParams& P) { return P.a.rows <= cu_count(); }
 
-template <int DT>
-static int launch_finish(const KParams& P, bool vec, bool deep, hipStream_t st)
-{
-    if (deep) {
-        // one workgroup per queue slot; those past the queued count leave at once
-        if (vec) k_deep<DT, true><<<P.a.rows, kFinThreads, 0, st>>>(P);
-        else k_deep<DT, false><<<P.a.rows, kFinThreads, 0, st>>>(P);
-        FIE_LAUNCH_CHECK("k_deep");
-        return FIE_OK;
-    }
-    const bool wide = finish_in_place(P);
-    if (vec) {
-        if (wide) k_finish<DT, true, true><<<P.a.rows, kFinThreads, 0, st>>>(P);
-        else k_finish<DT, true, false><<<P.a.rows, kFinThreads, 0, st>>>(P);
-    } else {
-        if (wide) k_finish<DT, false, true><<<P.a.rows, kFinThreads, 0, st>>>(P);
-        else k_finish<DT, false, false><<<P.a.rows, kFinThreads, 0, st>>>(P);
-    }
-    FIE_LAUNCH_CHECK("k_finish");
-    return FIE_OK;
-}
-
 static int run_stage(const KParams& P, int stage, hipStream_t st)
 {
     const int sz = P.a.dtype == FIE_F32 ? 4 : 2;
@@ -329,38 +349,22 @@ static int run_stage(const KParams& P, int stage, hipStream_t st)
         }
         return FIE_OK;
     }
+    hipError_t e;
+    const char* what;
     if (stage == FIE_STAGE_SCAN) {
-        switch (P.a.dtype) {
-        case FIE_F32: return launch_scan<FIE_F32>(P, vec, longh, st);
-        case FIE_F16: return launch_scan<FIE_F16>(P, vec, longh, st);
-        default: return launch_scan<FIE_BF16>(P, vec, longh, st);
-        }
-    }
-    const bool deep = stage == FIE_STAGE_DEEP;
-    switch (P.a.dtype) {
-    case FIE_F32: return launch_finish<FIE_F32>(P, vec, deep, st);
-    case FIE_F16: return launch_finish<FIE_F16>(P, vec, deep, st);
-    default: return launch_finish<FIE_BF16>(P, vec, deep, st);
-    }
-}
-
-template <int DT>
-static int launch_lmhead(const KParams& P, const void* hidden, const void* weight, int H, bool vec, bool longh,
-                         hipStream_t st)
-{
-    const int nrb = (P.a.rows + kLhRows - 1) / kLhRows;
-    const int grid = 8 * ((P.NT + 7) / 8) * nrb;
-    const uint16_t* h = (const uint16_t*)hidden;
-    const uint16_t* w = (const uint16_t*)weight;
-    if (vec) {
-        if (longh) k_lmhead<DT, true, true><<<grid, kLhThreads, 0, st>>>(P, h, w, H, nrb);
-        else k_lmhead<DT, true, false><<<grid, kLhThreads, 0, st>>>(P, h, w, H, nrb);
+        e = launch_scan(P, vec, longh, st);
+        what = "k_scan";
     } else {
-        if (longh) k_lmhead<DT, false, true><<<grid, kLhThreads, 0, st>>>(P, h, w, H, nrb);
-        else k_lmhead<DT, false, false><<<grid, kLhThreads, 0, st>>>(P, h, w, H, nrb);
+        const bool deep = stage == FIE_STAGE_DEEP;
+        const bool wide = finish_in_place(P);
+        switch (P.a.dtype) {
+        case FIE_F32: e = launch_finish_f32(P, vec, deep, wide, st); break;
+        case FIE_F16: e = launch_finish_f16(P, vec, deep, wide, st); break;
+        default: e = launch_finish_bf16(P, vec, deep, wide, st); break;
+        }
+        what = deep ? "k_deep" : "k_finish";
     }
-    FIE_LAUNCH_CHECK("k_lmhead");
-    return FIE_OK;
+    return launch_status(e, what);
 }
 
 static int prepare(const fie_sampler_args* args, const fie_workspace* ws, KParams* P)
@@ -450,8 +454,7 @@ static int lmhead_run(const fie_sampler_args* args, const void* hidden, const vo
     }
     const bool vec = vec_ok(args->logits, args->row_stride, 2);
     const bool longh = args->apply_penalties && args->max_row_hist > 65535;
-    rc = args->dtype == FIE_F16 ? launch_lmhead<FIE_F16>(P, hidden, weight, hidden_dim, vec, longh, st)
-                                : launch_lmhead<FIE_BF16>(P, hidden, weight, hidden_dim, vec, longh, st);
+    rc = launch_status(launch_lmhead(P, hidden, weight, hidden_dim, vec, longh, st), "k_lmhead");
     if (rc != FIE_OK || !whole) return rc;
     rc = run_stage(P, FIE_STAGE_FINISH, st);
     if (rc != FIE_OK || finish_in_place(P)) return rc;

@@ -244,57 +244,6 @@ struct ScanSmem {
     uint32_t uniq[kWavesPerWG];
 };
 
-// ---------------------------------------------------------------- k_prep
-// Buckets the history of every penalised row by span (sampler.py:134-144 counts
-// the same ids): the offsets inside the span of the first kBucketCap ids of each
-// span, the number of ids per span, the occurrences of token 0 and of ids >= vocab.
-// Each k_scan workgroup then reads its own span's bucket instead of the whole
-// history.  The order inside a bucket is free: only counts are taken from it.
-__global__ __launch_bounds__(kPrepThreads) void k_prep(const KParams P)
-{
-    __shared__ uint32_t sc[kMaxSpans];
-    __shared__ uint32_t zc, badc;
-    const fie_sampler_args& a = P.a;
-    const int row = blockIdx.x, tid = threadIdx.x, NS = P.NS;
-    const uint32_t V = (uint32_t)a.vocab;
-    // the row's flags and history range are loaded together (one round trip)
-    const int32_t fl = a.flags[row];
-    const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
-    if (!(a.apply_penalties && (fl & FIE_FLAG_PENALTY))) return;
-    if (tid < NS) sc[tid] = 0;
-    if (tid == 0) { zc = 0; badc = 0; }
-    __syncthreads();
-    uint16_t* bk = P.w.bk + (size_t)row * NS * kBucketCap;
-    constexpr int kPer = 8;   // ids per thread per batch, loaded together
-    for (int64_t base = h0; base < h1; base += (int64_t)kPer * kPrepThreads) {
-        uint32_t ids[kPer];
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            const int64_t h = base + q * kPrepThreads + tid;
-            ids[q] = h < h1 ? (uint32_t)a.hist_ids[h] : 0xFFFFFFFFu;
-        }
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            const uint32_t id = ids[q];
-            if (id == 0) {
-                atomicAdd(&zc, 1u);
-            } else if (id < V) {
-                const uint32_t sp = id / (uint32_t)kSpan;
-                const uint32_t at = atomicAdd(&sc[sp], 1u);
-                if (at < (uint32_t)kBucketCap) bk[sp * kBucketCap + at] = (uint16_t)(id % (uint32_t)kSpan);
-            } else if (base + q * kPrepThreads + tid < h1) {
-                atomicAdd(&badc, 1u);
-            }
-        }
-    }
-    __syncthreads();
-    if (tid < NS) P.w.nb[(size_t)row * NS + tid] = sc[tid];
-    if (tid == 0) {
-        P.w.tok0c[row] = zc;
-        P.w.bad[row] = badc;
-    }
-}
-
 // Per-row settings the tile pass reads (sampler.py:182 leaves greedy rows unscaled).
 struct RowCfg {
     bool greedy, pen, need_mass, need_cand;
@@ -384,12 +333,10 @@ FIE_DEV void scan_tile(const KParams& P, const RowCfg& rc, int row, int tile,
             }
         } else if (__ballot(mine != 0) != 0) {
             // a set bit ORs a quiet NaN's exponent and quiet bit into the value
-#ifndef FIE_X_NOMARK
 #pragma unroll
             for (int i = 0; i < kEPT; ++i)
                 x[i] = __int_as_float(__float_as_int(x[i]) |
                                       (__builtin_amdgcn_sbfe((int)mine, (unsigned)i, 1u) & 0x7FC00000));
-#endif
             uint32_t b = mine;
 #pragma unroll
             for (int q = 0; q < kPS; ++q) {
@@ -400,11 +347,7 @@ FIE_DEV void scan_tile(const KParams& P, const RowCfg& rc, int row, int tile,
             }
 #pragma unroll
             for (int q = 0; q < kPS; ++q)
-#ifndef FIE_X_NOLOAD
                 if (pidx[q] != 0xFFFFFFFFu) pv[q] = load_elem<DT>(rowp, pidx[q]);
-#else
-                if (pidx[q] != 0xFFFFFFFFu) pv[q] = 1.0f;
-#endif
 #pragma unroll
             for (int q = 0; q < kPS; ++q)
                 if (pidx[q] != 0xFFFFFFFFu) pv[q] = penalize(pv[q], rep, pres, freq, count_of((int)pidx[q] - pbase));
@@ -676,10 +619,6 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
                 atomicAdd(&L.uniq[o / kTile], 1u);
             }
         };
-#ifdef FIE_X_NOCOUNT
-        if (nb <= (uint32_t)kBucketCap) {
-        } else
-#endif
         if (nb <= (uint32_t)kBucketCap) {
             if ((uint32_t)tid < nb) count(e0);
             for (uint32_t i = tid + kScanThreads; i < nb; i += kScanThreads) count(P.w.bk[rs * kBucketCap + i]);

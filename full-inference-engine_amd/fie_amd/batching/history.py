@@ -8,9 +8,13 @@ step (engine/batching/continuous_batching.py:1920-1925 passes prompt + output).
 uploads only what was appended since the request's last step; the kernels read
 each row's [start, end) range of that array (``fie_sampler_args.hist_ends``).
 
-A context that is not an extension of the stored one (shorter, or a different
-token where the stored one ends) is stored afresh, so a preempted and rebuilt
-request still samples from exactly the context it passes.
+Contract: a request id's context only grows between steps (prompt + output, as
+the engine builds it), or the id is forgotten (``forget``) before its context
+changes otherwise.  Cheap probes catch the usual violations and store such a
+context afresh: a context shorter than the stored one, a change among the last
+kTail stored tokens (a rollback), or at the first token or at three positions
+fixed when the context was stored (a reused id).  A change elsewhere in a long
+context is not detected in O(1) per row.
 """
 
 from __future__ import annotations
@@ -19,18 +23,51 @@ import numpy as np
 import torch
 
 
+kTail = 8   # stored tokens compared at every step, counted from the end
+
+
 class _Slot:
-    __slots__ = ("start", "cap", "length", "last", "vocab", "bigs", "zero", "late")
+    __slots__ = ("start", "cap", "length", "tail", "probes", "vocab", "bigs", "zero", "late")
 
     def __init__(self, start: int, cap: int, vocab: int):
-        self.start, self.cap, self.length, self.last, self.vocab = start, cap, 0, -1, vocab
+        self.start, self.cap, self.length, self.vocab = start, cap, 0, vocab
+        self.tail: list[int] = []                  # the last kTail stored ids
+        self.probes: tuple = ()                    # (position, id) pairs fixed at storing
         self.bigs: set[int] = set()   # distinct ids >= vocab seen
         self.zero: int | None = None  # position of the first token 0
         self.late = False             # an id >= vocab first occurs after the first 0
 
+    def extended_by(self, ctx: list[int], n: int) -> bool:
+        """Whether ctx (length n) holds the stored context as its prefix, by the
+        probes of the module contract."""
+        ln = self.length
+        if n < ln:
+            return False
+        if ln == 0:
+            return True
+        if ctx[max(ln - kTail, 0):ln] != self.tail:
+            return False
+        for at, v in self.probes:
+            if ctx[at] != v:
+                return False
+        return True
+
+    def stored(self, ctx: list[int], n: int) -> None:
+        """Record that ctx[:n] is now the stored context."""
+        if self.length == 0 and n:
+            self.probes = tuple((at, ctx[at]) for at in sorted({0, n // 4, n // 2, (3 * n) // 4}) if at < n)
+        self.length = n
+        self.tail = ctx[max(n - kTail, 0):n]
+
 
 class DeviceHistory:
-    """Per-request contexts in one int32 device array (a bump arena)."""
+    """Per-request contexts in one int32 device array (a bump arena).
+
+    A step first decides, for every row, whether its request needs fresh space (a
+    new context, or one that outgrew its slot), then makes room for all of it at
+    once (growing or compacting the array, which moves slots), and only then hands
+    out space and records the rows' ranges and write positions: nothing recorded in
+    a step can be moved by a later row of the same step."""
 
     # set once any stored context holds an id >= vocab: only then do rows need the
     # out-of-vocabulary scan of update()
@@ -44,12 +81,11 @@ class DeviceHistory:
         self.slots: dict[object, _Slot] = {}
 
     # ------------------------------------------------------------------ storage
-    def _reserve(self, n: int) -> int:
-        """Start of n free ints, growing (or compacting) the array when full."""
+    def _make_room(self, n: int) -> None:
+        """Ensure n free ints past `top`, growing (or compacting) the array; live
+        slots may move (their `start` is updated)."""
         if self.top + n <= self.ids.numel():
-            at = self.top
-            self.top += n
-            return at
+            return
         size = max(2 * self.ids.numel(), 2 * (self.live + n))
         fresh = torch.empty(size, dtype=torch.int32, device=self.device)
         if self.top - self.live > self.live:
@@ -63,23 +99,34 @@ class DeviceHistory:
         else:
             fresh[:self.top].copy_(self.ids[:self.top])
         self.ids = fresh
+
+    def _bump(self, n: int) -> int:
+        """Start of n free ints; _make_room has reserved them (nothing moves)."""
         at = self.top
         self.top += n
+        if self.top > self.ids.numel():
+            raise AssertionError("DeviceHistory: space handed out beyond the room made for the step")
         return at
 
-    def _new_slot(self, rid: object, need: int, vocab: int) -> _Slot:
+    @staticmethod
+    def _new_cap(n: int) -> int:
+        return max(256, 2 * n)
+
+    @staticmethod
+    def _grow_cap(slot: _Slot, n: int) -> int:
+        return max(2 * slot.cap, 2 * n)
+
+    def _new_slot(self, rid: object, cap: int, vocab: int) -> _Slot:
         old = self.slots.pop(rid, None)
         if old is not None:
             self.live -= old.cap
-        cap = max(256, 2 * need)
-        slot = _Slot(self._reserve(cap), cap, vocab)
+        slot = _Slot(self._bump(cap), cap, vocab)
         self.slots[rid] = slot
         self.live += cap
         return slot
 
-    def _grow(self, slot: _Slot, need: int) -> None:
-        cap = max(2 * slot.cap, 2 * need)
-        start = self._reserve(cap)
+    def _grow(self, slot: _Slot, cap: int) -> None:
+        start = self._bump(cap)
         self.ids[start:start + slot.length].copy_(self.ids[slot.start:slot.start + slot.length])
         self.live += cap - slot.cap
         slot.start, slot.cap = start, cap
@@ -116,42 +163,59 @@ class DeviceHistory:
         ends, hist_invalid or None, longest, write_dst, write_src): the rows'
         ranges in ``ids`` and the appended tokens still to be written there.
 
-        One pass per row decides each row's slot and gathers its appended ids into
-        one list; the range check and the token-0 scan then run once over all of
-        them, and the slots advance only after the check passes."""
+        One pass decides each row's action and the room the step needs; after the
+        room is made, a second pass hands out space and gathers the appended ids
+        into one list; the range check and the token-0 scan then run once over all
+        of them, and the slots advance only after the check passes."""
         rows = len(contexts)
         sel = np.flatnonzero(include).tolist()
         picked = [request_ids[r] for r in sel]
         if len(set(picked)) != len(picked):
             # one request twice in a batch: rows see each other's appends in order
             return self._update_rowwise(contexts, include, request_ids, vocab)
-        starts_l = [0] * rows
-        ends_l = [0] * rows
-        longest = 0
-        flat: list[int] = []
-        moved = []            # (slot, old length, new length, last id) of rows that grew
-        counts, bases = [], []
         get = self.slots.get
-        extend, c_append, b_append, m_append = flat.extend, counts.append, bases.append, moved.append
+        # pass 1: each row's action (0 keep, 1 new slot, 2 grow) and the room needed
+        acts = []
+        need = 0
         for r, rid in zip(sel, picked):
             ctx = contexts[r]
             n = len(ctx)
             slot = get(rid)
-            if slot is None:
-                slot = self._new_slot(rid, n, vocab)
+            if slot is None or slot.vocab != vocab or not slot.extended_by(ctx, n):
+                cap = self._new_cap(n)
+                acts.append((1, cap))
+                need += cap
+            elif n > slot.cap:
+                cap = self._grow_cap(slot, n)
+                acts.append((2, cap))
+                need += cap
             else:
-                ln = slot.length
-                if slot.vocab != vocab or n < ln or (ln and ctx[ln - 1] != slot.last):
-                    slot = self._new_slot(rid, n, vocab)
-                elif n > slot.cap:
-                    self._grow(slot, n)
+                acts.append((0, 0))
+        self._make_room(need)
+        # pass 2: space handed out (nothing moves now), appended ids gathered
+        starts_l = [0] * rows
+        ends_l = [0] * rows
+        longest = 0
+        flat: list[int] = []
+        moved = []            # (slot, old length, new length, context) of rows that grew
+        counts, bases = [], []
+        extend, c_append, b_append, m_append = flat.extend, counts.append, bases.append, moved.append
+        for (r, rid), (act, cap) in zip(zip(sel, picked), acts):
+            ctx = contexts[r]
+            n = len(ctx)
+            if act == 1:
+                slot = self._new_slot(rid, cap, vocab)
+            else:
+                slot = self.slots[rid]
+                if act == 2:
+                    self._grow(slot, cap)
             ln = slot.length
             st = slot.start
             if n > ln:
                 extend(ctx[ln:])
                 c_append(n - ln)
                 b_append(st + ln)
-                m_append((slot, ln, n, ctx[-1]))
+                m_append((slot, ln, n, ctx))
             starts_l[r] = st
             ends_l[r] = st + n
             if n > longest:
@@ -172,9 +236,8 @@ class DeviceHistory:
                 for i in np.unique(seg[odd]).tolist():
                     slot, old, _, _ = moved[i]
                     self._note(slot, new[first[i]:first[i] + cnt[i]], vocab, base=old)
-            for slot, _, n, last in moved:
-                slot.length = n
-                slot.last = int(last)
+            for slot, _, n, ctx in moved:
+                slot.stored(ctx, n)
         else:
             dst = np.zeros(0, np.int64)
             src = np.zeros(0, np.int32)
@@ -191,8 +254,35 @@ class DeviceHistory:
 
     def _update_rowwise(self, contexts: list[list[int]], include: np.ndarray,
                         request_ids: list[object], vocab: int):
-        """update() one row after another (a request that appears twice)."""
+        """update() one row after another (a request that appears twice).  The room
+        is made first for the allocations a dry run of the rows predicts, so no
+        slot moves while rows are recorded, and a slot one row replaces keeps its
+        memory until the step ends."""
         rows = len(contexts)
+        # dry run: per request, (cap, length, vocab, context) as the rows leave it
+        sim: dict[object, tuple] = {}
+        need = 0
+        for r in range(rows):
+            if not include[r]:
+                continue
+            ctx = contexts[r]
+            n = len(ctx)
+            rid = request_ids[r]
+            if rid in sim:
+                cap, ln, voc, prev = sim[rid]
+                ext = voc == vocab and n >= ln and ctx[:ln] == prev[:ln]
+            else:
+                slot = self.slots.get(rid)
+                cap = slot.cap if slot is not None else 0
+                ext = slot is not None and slot.vocab == vocab and slot.extended_by(ctx, n)
+            if not ext:
+                cap = self._new_cap(n)
+                need += cap
+            elif n > cap:
+                cap = max(2 * cap, 2 * n)
+                need += cap
+            sim[rid] = (cap, n, vocab, ctx)
+        self._make_room(need)
         starts = np.zeros(rows, dtype=np.int64)
         ends = np.zeros(rows, dtype=np.int64)
         invalid = np.zeros(rows, dtype=np.int32)
@@ -205,11 +295,10 @@ class DeviceHistory:
             n = len(ctx)
             rid = request_ids[r]
             slot = self.slots.get(rid)
-            if (slot is None or slot.vocab != vocab or n < slot.length
-                    or (slot.length and ctx[slot.length - 1] != slot.last)):
-                slot = self._new_slot(rid, n, vocab)
+            if slot is None or slot.vocab != vocab or not slot.extended_by(ctx, n):
+                slot = self._new_slot(rid, self._new_cap(n), vocab)
             elif n > slot.cap:
-                self._grow(slot, n)
+                self._grow(slot, self._grow_cap(slot, n))
             if n > slot.length:
                 new = np.asarray(ctx[slot.length:], dtype=np.int64)
                 if new.min() < 0 or new.max() >= 2**31:
@@ -217,8 +306,7 @@ class DeviceHistory:
                 self._note(slot, new, vocab)
                 dst_parts.append(np.arange(slot.start + slot.length, slot.start + n, dtype=np.int64))
                 src_parts.append(new.astype(np.int32))
-                slot.length = n
-                slot.last = int(ctx[-1])
+                slot.stored(ctx, n)
             starts[r] = slot.start
             ends[r] = slot.start + n
             if slot.bigs:

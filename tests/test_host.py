@@ -181,14 +181,88 @@ def test_device_history_duplicate_rows_and_rejected_ids():
     for r, ctx in enumerate([a_ctx, b_ctx, a_ctx]):
         np.testing.assert_array_equal(h.ids[starts[r]:ends[r]].numpy(), np.array(ctx, dtype=np.int32))
     assert invalid is not None and invalid[1] == 1 | (1 << 30) and invalid[0] == invalid[2] == 0
-    before = {rid: (s.start, s.length, s.last) for rid, s in h.slots.items()}
+    before = {rid: (s.start, s.length, tuple(s.tail)) for rid, s in h.slots.items()}
     with pytest.raises(ValueError):
         h.update([a_ctx + [5], b_ctx + [-1]], np.ones(2, bool), ["a", "b"], vocab)
-    assert {rid: (s.start, s.length, s.last) for rid, s in h.slots.items()} == before
+    assert {rid: (s.start, s.length, tuple(s.tail)) for rid, s in h.slots.items()} == before
     starts, ends, _, _, dst, src = h.update([a_ctx + [5], b_ctx + [6]], np.ones(2, bool), ["a", "b"], vocab)
     assert dst.size == 2
     h.ids[torch.from_numpy(dst)] = torch.from_numpy(src)
     np.testing.assert_array_equal(h.ids[starts[1]:ends[1]].numpy(), np.array(b_ctx + [6], dtype=np.int32))
+
+
+def _check_ranges(h, contexts, include, starts, ends, dst, src):
+    """Apply the appends as k_history_write does, then every included row's range
+    must hold exactly its context."""
+    import torch
+    h.ids[torch.from_numpy(dst)] = torch.from_numpy(src)
+    for r, ctx in enumerate(contexts):
+        if include[r]:
+            np.testing.assert_array_equal(h.ids[starts[r]:ends[r]].numpy(), np.array(ctx, dtype=np.int32))
+
+
+def test_device_history_compaction_inside_one_batch():
+    """A batch whose later rows need fresh space after most stored contexts were
+    forgotten: the array is compacted (slots move) before any row's range or write
+    position is recorded, so every row, the earlier ones included, reads exactly its
+    context and each appended token lands inside its row's range."""
+    import torch
+    from fie_amd.batching.history import DeviceHistory
+
+    vocab = 100
+    h = DeviceHistory(torch.device("cpu"), capacity=1024)
+    first = {"x1": [1] * 10, "x2": [2] * 10, "x3": [3] * 10, "a": [4, 5, 6]}
+    ids = list(first)
+    ctxs = [first[k] for k in ids]
+    inc = np.ones(len(ids), bool)
+    starts, ends, _, _, dst, src = h.update(ctxs, inc, ids, vocab)
+    _check_ranges(h, ctxs, inc, starts, ends, dst, src)
+    assert h.slots["a"].start == 768                     # behind three 256-int slots
+    h.forget(["x1", "x2", "x3"])
+    # 'a' appends one token (recorded first), 'b' is new and does not fit: compaction
+    ctxs = [[4, 5, 6, 7], list(range(300))]
+    ids = ["a", "b"]
+    inc = np.ones(2, bool)
+    starts, ends, _, _, dst, src = h.update(ctxs, inc, ids, vocab)
+    assert h.slots["a"].start == 0                       # 'a' moved down
+    assert starts[0] == h.slots["a"].start and ends[0] == starts[0] + 4
+    assert starts[0] <= dst[0] < ends[0]
+    _check_ranges(h, ctxs, inc, starts, ends, dst, src)
+
+
+def test_device_history_detects_a_changed_prefix():
+    """A stored context is reused only when the new one extends it: a context of
+    the same request id that keeps the stored last token but differs earlier (a
+    reused id), or that rolls back and regrows, is stored afresh."""
+    import torch
+    from fie_amd.batching.history import DeviceHistory
+
+    vocab = 50
+    h = DeviceHistory(torch.device("cpu"), capacity=4096)
+    inc = np.ones(1, bool)
+    for old, new in (([1, 2, 3], [9, 9, 3, 4]),                       # differs before the last token
+                     (list(range(40)), list(range(30)) + [7] * 9 + [39, 40]),   # rollback, regrown
+                     (list(range(40)), [5] + list(range(1, 41)))):     # the first token changed
+        h.forget(["q"])
+        starts, ends, _, _, dst, src = h.update([old], inc, ["q"], vocab)
+        _check_ranges(h, [old], inc, starts, ends, dst, src)
+        starts, ends, _, _, dst, src = h.update([new], inc, ["q"], vocab)
+        assert dst.size == len(new)                                    # stored afresh
+        _check_ranges(h, [new], inc, starts, ends, dst, src)
+
+
+def test_device_history_rowwise_replacement_keeps_earlier_rows():
+    """One request twice in a batch with a context the second row does not extend:
+    the first row's range stays readable (its slot is not reused in the step)."""
+    import torch
+    from fie_amd.batching.history import DeviceHistory
+
+    vocab = 50
+    h = DeviceHistory(torch.device("cpu"), capacity=300)
+    ctxs = [[1, 2, 3, 4], [7, 8], [1, 2, 3, 4, 5]]
+    inc = np.ones(3, bool)
+    starts, ends, _, _, dst, src = h.update(ctxs, inc, ["a", "a", "b"], vocab)
+    _check_ranges(h, ctxs, inc, starts, ends, dst, src)
 
 
 # ---------------------------------------------------------------- the adapter's calls
