@@ -802,11 +802,20 @@ static_assert(kMaxTiles < kFinThreads, "the last thread is free for token 0");
 // to the floors of R1 and the exponentials' rounding (used only to narrow).
 FIE_DEV float approx_mass(float y, float M) { return __expf(y - M); }
 
-// The x-domain candidate slot as a y-domain composite.
-FIE_DEV uint64_t cand_y(uint64_t xc, float s)
+// The x-domain candidate slot as a y-domain composite.  rs = 1/s when s lies in
+// Markstein's range (cand_rs), else 0: inside the range the corrected product is
+// the IEEE quotient, three operations instead of the divide's sequence.
+FIE_DEV uint64_t cand_y(uint64_t xc, float s, float rs)
 {
-    return comp_key(fkey(y_of_xkey(comp_k(xc), s)), comp_idx(xc));
+    const float x = key_to_float(comp_k(xc));
+    float y;
+    if (s == 1.0f) y = x;
+    else if (rs != 0.0f && markstein_ok(x)) y = div_markstein(x, s, rs) + 0.0f;
+    else y = scaled(x, s);
+    return comp_key(fkey(y), comp_idx(xc));
 }
+
+FIE_DEV float cand_rs(float s) { return (s != 1.0f && s >= 0x1p-30f && s <= 0x1p30f) ? 1.0f / s : 0.0f; }
 
 // Q held y-domain composites per thread (those with ok set): the largest is tracked;
 // those whose key exceeds `safe` join S.cand (at most kGCap stored, all counted in
@@ -860,8 +869,9 @@ FIE_DEV void cand_batch(FinSmem& S, const KParams& P, int row, int NT, int t0, f
         ok[q] = t < NT && (uint32_t)lane < S.nc[t];
         cv[q] = ok[q] ? P.w.cand[((size_t)row * NT + t) * kCapW + lane] : 0ull;
     }
+    const float rs = cand_rs(s);
 #pragma unroll
-    for (int q = 0; q < Q; ++q) cv[q] = ok[q] ? cand_y(cv[q], s) : 0ull;
+    for (int q = 0; q < Q; ++q) cv[q] = ok[q] ? cand_y(cv[q], s, rs) : 0ull;
     ok[Q] = with0 && tid == kFinThreads - 1;
     cv[Q] = z0;
     cand_commit(S, cv, ok, safe, best, bins, M);
@@ -1311,12 +1321,13 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
     if (spec) {
         uint64_t best = 0;
         {
+            const float rs = cand_rs(s);
             bool ok[Q + 1];
 #pragma unroll
             for (int q = 0; q < Q; ++q) {
                 const int t = wave + kFinWaves * q;
                 ok[q] = t < NT && (uint32_t)lane < S.nc[t];
-                xs[q] = ok[q] ? cand_y(xs[q], s) : 0ull;
+                xs[q] = ok[q] ? cand_y(xs[q], s, rs) : 0ull;
             }
             ok[Q] = tid == kFinThreads - 1;
             xs[Q] = comp_key(k0, 0);

@@ -19,6 +19,8 @@ context is not detected in O(1) per row.
 
 from __future__ import annotations
 
+import operator
+
 import numpy as np
 import torch
 
@@ -27,12 +29,14 @@ kTail = 8   # stored tokens compared at every step, counted from the end
 
 
 class _Slot:
-    __slots__ = ("start", "cap", "length", "tail", "probes", "vocab", "bigs", "zero", "late")
+    __slots__ = ("start", "cap", "length", "tail", "probe_get", "probe_vals", "vocab", "bigs",
+                 "zero", "late")
 
     def __init__(self, start: int, cap: int, vocab: int):
         self.start, self.cap, self.length, self.vocab = start, cap, 0, vocab
         self.tail: list[int] = []                  # the last kTail stored ids
-        self.probes: tuple = ()                    # (position, id) pairs fixed at storing
+        self.probe_get = None                      # itemgetter of the positions fixed at storing
+        self.probe_vals: tuple = ()                # the ids stored there
         self.bigs: set[int] = set()   # distinct ids >= vocab seen
         self.zero: int | None = None  # position of the first token 0
         self.late = False             # an id >= vocab first occurs after the first 0
@@ -45,19 +49,20 @@ class _Slot:
             return False
         if ln == 0:
             return True
-        if ctx[max(ln - kTail, 0):ln] != self.tail:
+        if ctx[ln - kTail if ln > kTail else 0:ln] != self.tail:
             return False
-        for at, v in self.probes:
-            if ctx[at] != v:
-                return False
-        return True
+        return self.probe_get(ctx) == self.probe_vals
 
     def stored(self, ctx: list[int], n: int) -> None:
         """Record that ctx[:n] is now the stored context."""
         if self.length == 0 and n:
-            self.probes = tuple((at, ctx[at]) for at in sorted({0, n // 4, n // 2, (3 * n) // 4}) if at < n)
+            at = sorted({0, n // 4, n // 2, (3 * n) // 4})
+            # two positions at least, so the getter always returns a tuple
+            at = at if len(at) > 1 else at * 2
+            self.probe_get = operator.itemgetter(*at)
+            self.probe_vals = self.probe_get(ctx)
         self.length = n
-        self.tail = ctx[max(n - kTail, 0):n]
+        self.tail = ctx[n - kTail if n > kTail else 0:n]
 
 
 class DeviceHistory:
@@ -173,6 +178,9 @@ class DeviceHistory:
         if len(set(picked)) != len(picked):
             # one request twice in a batch: rows see each other's appends in order
             return self._update_rowwise(contexts, include, request_ids, vocab)
+        fast = self._update_fast(contexts, sel, picked, rows, vocab)
+        if fast is not None:
+            return fast
         get = self.slots.get
         # pass 1: each row's action (0 keep, 1 new slot, 2 grow) and the room needed
         acts = []
@@ -220,6 +228,49 @@ class DeviceHistory:
             ends_l[r] = st + n
             if n > longest:
                 longest = n
+        return self._finish_update(contexts, sel, picked, rows, vocab, starts_l, ends_l, longest,
+                                   flat, counts, bases, moved)
+
+    def _update_fast(self, contexts, sel, picked, rows, vocab):
+        """update() when every row's request has a slot holding a prefix of its
+        context with room for the rest (the steady state of decoding): one pass and
+        no slot moves; None when some row needs a new or larger slot."""
+        get = self.slots.get
+        starts_l = [0] * rows
+        ends_l = [0] * rows
+        longest = 0
+        flat: list[int] = []
+        moved = []
+        counts, bases = [], []
+        extend, c_append, b_append, m_append = flat.extend, counts.append, bases.append, moved.append
+        for r, rid in zip(sel, picked):
+            ctx = contexts[r]
+            n = len(ctx)
+            slot = get(rid)
+            if slot is None or slot.vocab != vocab or n > slot.cap:
+                return None
+            ln = slot.length
+            if ln:
+                if n < ln or ctx[ln - kTail if ln > kTail else 0:ln] != slot.tail \
+                        or slot.probe_get(ctx) != slot.probe_vals:
+                    return None
+            st = slot.start
+            if n > ln:
+                extend(ctx[ln:])
+                c_append(n - ln)
+                b_append(st + ln)
+                m_append((slot, ln, n, ctx))
+            starts_l[r] = st
+            ends_l[r] = st + n
+            if n > longest:
+                longest = n
+        return self._finish_update(contexts, sel, picked, rows, vocab, starts_l, ends_l, longest,
+                                   flat, counts, bases, moved)
+
+    def _finish_update(self, contexts, sel, picked, rows, vocab, starts_l, ends_l, longest,
+                       flat, counts, bases, moved):
+        """The common tail of update(): range check and token-0 bookkeeping over all
+        appended ids at once, then the slots advance."""
         starts = np.array(starts_l, dtype=np.int64)
         ends = np.array(ends_l, dtype=np.int64)
         if flat:

@@ -251,8 +251,11 @@ class BatchedSampler:
         if rows == 0:
             return SampleResult([], {})
 
-        wants_logprobs = any(p.logprobs is not None for p in params)
-        plain = all(p.greedy and not p.has_penalties for p in params)
+        # the per-row predicates from one pass over the params (reused while a decode
+        # loop passes the same SamplingParams objects)
+        t = param_table(params)
+        wants_logprobs = bool((t.lp >= 0).any())
+        plain = bool((t.greedy & ~t.pen).all())
         if plain and not wants_logprobs:
             # sampler.py:103-106: one argmax kernel and one device-to-host copy.
             return SampleResult(self._fused.argmax(logits).tolist(), {})
@@ -261,8 +264,8 @@ class BatchedSampler:
                             rng=self._draw_keys(params, request_ids),
                             history=self._history, request_ids=request_ids)
         out, _, _ = self._fused.step(logits, hp)
-        tokens = [int(t) for t in out["tokens"]]
-        return SampleResult(tokens, self._logprobs(params, tokens, out))
+        tokens = out["tokens"].tolist()
+        return SampleResult(tokens, self._logprobs(params, tokens, out) if wants_logprobs else {})
 
     @staticmethod
     def _logprobs(params: list[SamplingParams], chosen: list[int],

@@ -521,3 +521,33 @@ def test_lmhead_long_history_counts(fs):
     two, _, _ = fs.step(logits, hp)
     for name in ("tokens", "status", "cut_comp", "row_max", "kept_mass", "row_mass"):
         np.testing.assert_array_equal(out[name], two[name], err_msg=name)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_queued_full_row_rows_match_the_oracle(fs, dtype):
+    """More rows than CUs, many of them deep (flat logits): top-p and plain rows, with
+    and without penalties, are queued by k_finish and settled by k_deep's full-row
+    passes; tokens, cuts, thresholds and kept masses equal the oracle's."""
+    rng = np.random.default_rng(77 + int(dtype == torch.bfloat16))
+    rows, vocab = 300, 50000
+    x = torch.from_numpy(rng.normal(0, 0.3, (rows, vocab)).astype(np.float32)).to(dtype)
+    pen = dict(repetition_penalty=1.2, frequency_penalty=0.3, presence_penalty=0.1)
+    params = []
+    for r in range(rows):
+        kind = r % 6
+        if kind == 0:
+            params.append(SamplingParams(temperature=1.0, top_p=0.95))
+        elif kind == 1:
+            params.append(SamplingParams(temperature=0.8, top_p=0.9, **pen))
+        elif kind == 2:
+            params.append(SamplingParams(temperature=1.0))
+        elif kind == 3:
+            params.append(SamplingParams(temperature=1.3, **pen))
+        elif kind == 4:
+            params.append(SamplingParams(temperature=1.0, top_p=0.5, top_k=3000))   # not split: top-k
+        else:
+            params.append(SamplingParams(**pen))                                    # greedy
+    ctx = [list(rng.integers(0, vocab, size=int(rng.integers(0, 3000)))) for _ in range(rows)]
+    out, ref, _, _ = run_both(fs, x, params, rng.random(rows), ctx, kept=False)
+    check(out, ref, params)
+    assert ((out["status"] & 1) != 0).sum() >= rows // 2, "the flat rows should take the full-row path"
