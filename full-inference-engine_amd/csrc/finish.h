@@ -854,6 +854,30 @@ FIE_DEV void cand_commit(FinSmem& S, const uint64_t (&cv)[Q], const bool (&ok)[Q
     }
 }
 
+// The first sweep of a two-sweep commit: the held composites above `safe` are
+// counted (S.n, one LDS atomic per wave) and binned by d-bin (count, and float mass
+// when `mass`), the largest tracked; nothing is stored.  Called by whole waves.
+template <int Q>
+FIE_DEV void cand_count(FinSmem& S, const uint64_t (&cv)[Q], const bool (&ok)[Q], uint32_t safe,
+                        uint64_t& best, bool mass, float M)
+{
+    uint32_t k = 0;
+#pragma unroll
+    for (int q = 0; q < Q; ++q) {
+        if (!ok[q]) continue;
+        best = cv[q] > best ? cv[q] : best;
+        if (comp_k(cv[q]) > safe) {
+            ++k;
+            const float y = key_to_float(comp_k(cv[q]));
+            const int b = dbin_y(M, y);
+            atomicAdd(&S.pc[b], 1u);
+            if (mass) atomicAdd(&S.pmf[b], approx_mass(y, M));
+        }
+    }
+    const uint32_t wk = wave_sum_u32(k);
+    if ((threadIdx.x & 63) == 0 && wk) atomicAdd(&S.n, wk);
+}
+
 // Tiles t0 + w + kFinWaves q (q < Q) of the row, and token 0 (composite z0) on the
 // last thread when `with0`: load, convert, commit.
 template <int Q>
@@ -914,7 +938,12 @@ FIE_DEV float wave_incl_scan_f32(float v)
 // 2^80) that covers the float sums' rounding and the floors of rule R1, so the
 // prefix it picks holds exact mass above g.  Should a crossing still fall past the
 // prefix, the exact selection finds no element there and reloads every candidate.
-FIE_DEV int narrow_binned(FinSmem& S, int nv, float M, int cnt, u128 g)
+// The last d-bin a narrowed prefix must keep, from the bins' counts (S.pc) and,
+// with use_mass, float masses (S.pmf): the bin where the running count reaches
+// cnt (cnt > 0) and the bin where the float prefix first exceeds g by the margin
+// described above, the later of the two; -1 when either is not found
+// (no narrowing).
+FIE_DEV int binned_bound(FinSmem& S, int cnt, bool use_mass, u128 g)
 {
     constexpr int per = kPassBins / kFinThreads;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -924,7 +953,7 @@ FIE_DEV int narrow_binned(FinSmem& S, int nv, float M, int cnt, u128 g)
 #pragma unroll
     for (int q = 0; q < per; ++q) {
         c[q] = S.pc[tid * per + q];
-        m[q] = S.pmf[tid * per + q];
+        m[q] = use_mass ? S.pmf[tid * per + q] : 0.0f;
         cs += c[q];
         ms += m[q];
     }
@@ -936,7 +965,7 @@ FIE_DEV int narrow_binned(FinSmem& S, int nv, float M, int cnt, u128 g)
     }
     if (tid == 0) {
         S.ibin = cnt > 0 ? -1 : 0;
-        S.flag = -1;
+        S.flag = use_mass ? -1 : 0;
         S.bcnt = 0;
     }
     __syncthreads();
@@ -952,14 +981,21 @@ FIE_DEV int narrow_binned(FinSmem& S, int nv, float M, int cnt, u128 g)
     for (int q = 0; q < per; ++q) {
         const int b = tid * per + q;
         if (cnt > 0 && crun < (uint32_t)cnt && crun + c[q] >= (uint32_t)cnt) S.ibin = b;
-        if (!(mrun > target) && mrun + m[q] > target) atomicMax(&S.flag, b);
+        if (use_mass && !(mrun > target) && mrun + m[q] > target) atomicMax(&S.flag, b);
         crun += c[q];
         mrun += m[q];
     }
     __syncthreads();
     const int bc = S.ibin, bm = S.flag;
-    if (bc < 0 || bm < 0) return nv;
-    const int bs = bc > bm ? bc : bm;
+    __syncthreads();
+    return (bc < 0 || bm < 0) ? -1 : (bc > bm ? bc : bm);
+}
+
+FIE_DEV int narrow_binned(FinSmem& S, int nv, float M, int cnt, u128 g)
+{
+    const int tid = threadIdx.x;
+    const int bs = binned_bound(S, cnt, true, g);
+    if (bs < 0) return nv;
     constexpr int kStage = kChunk / 2;           // S.cnt holds this many composites
     uint64_t* tmp = (uint64_t*)S.cnt;
     for (int i = tid; i < nv; i += kFinThreads) {
@@ -979,6 +1015,7 @@ FIE_DEV int narrow_binned(FinSmem& S, int nv, float M, int cnt, u128 g)
 
 // ---------------------------------------------------------------- sorted candidates
 constexpr int kSortMax = kGCap;    // candidates sorted in LDS, at most
+constexpr int kNarrowRegs = 128;   // two-sweep commits narrow from this many candidates on
 constexpr int kRankSort = 256;     // up to this many sort by rank (two or more threads each), more by bitonic merges
 
 // v of lane (lane ^ J): DPP moves inside rows of 16 lanes (quad permutes for 1 and
@@ -1234,7 +1271,12 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
     const bool spec = PH == 0 && need_cand;
     // rows narrowed by mass (no top-k, no min-p) bin their candidates as they are taken
     const bool bins = spec && !greedy && topk == 0 && !(mp > 0.0f);
-    if (bins) {
+    // rows narrowed by count (top-k, top-L) whose every tile's slots are held in
+    // registers commit their candidates in two sweeps: count and bin them, then
+    // store only the narrowed prefix (for rows narrowed by mass, committing all and
+    // compacting measured faster)
+    const bool regs = spec && !bins && NT <= kFinWaves * Q;
+    if (bins || regs) {
         for (int i = tid; i < kPassBins; i += kFinThreads) {
             S.pc[i] = 0;
             S.pmf[i] = 0.0f;
@@ -1318,23 +1360,25 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
 
     // PH 0: the candidates as y-domain composites, those above the safety key into
     // S.cand (binned when narrowed by mass); tiles past the held ones load now.
+    bool okr[Q + 1];             // the held slots, for the second sweep
     if (spec) {
         uint64_t best = 0;
         {
             const float rs = cand_rs(s);
-            bool ok[Q + 1];
 #pragma unroll
             for (int q = 0; q < Q; ++q) {
                 const int t = wave + kFinWaves * q;
-                ok[q] = t < NT && (uint32_t)lane < S.nc[t];
-                xs[q] = ok[q] ? cand_y(xs[q], s, rs) : 0ull;
+                okr[q] = t < NT && (uint32_t)lane < S.nc[t];
+                xs[q] = okr[q] ? cand_y(xs[q], s, rs) : 0ull;
             }
-            ok[Q] = tid == kFinThreads - 1;
+            okr[Q] = tid == kFinThreads - 1;
             xs[Q] = comp_key(k0, 0);
-            cand_commit(S, xs, ok, safe, best, bins, M);
+            if (regs) cand_count(S, xs, okr, safe, best, bins, M);
+            else cand_commit(S, xs, okr, safe, best, bins, M);
         }
-        for (int t0 = kFinWaves * Q; t0 < NT; t0 += kFinWaves * Q)
-            cand_batch<Q>(S, P, row, NT, t0, s, safe, best, bins, M, false, 0ull);
+        if (!regs)
+            for (int t0 = kFinWaves * Q; t0 < NT; t0 += kFinWaves * Q)
+                cand_batch<Q>(S, P, row, NT, t0, s, safe, best, bins, M, false, 0ull);
         best = wave_max_u64(best);
         if (lane == 0 && best) atomicMax((unsigned long long*)&S.cmax, (unsigned long long)best);
     }
@@ -1420,8 +1464,29 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
                 if (by_mass && sall == 0) narrow = false;
             }
             nvall = nv;
-            if (narrow && (cnt > 0 || by_mass))
+            if (regs) {
+                // second sweep: only the composites in bins up to the bound the
+                // selections can reach go to S.cand (narrowing is cheap here, so
+                // rows narrow from kNarrowRegs candidates on)
+                int bs = kPassBins;
+                if (nv > kNarrowRegs && (cnt > 0 || by_mass) && !(mp > 0.0f) && !(by_mass && sall == 0)) {
+                    const int b = binned_bound(S, cnt, by_mass, g);
+                    if (b >= 0) bs = b;
+                }
+                if (tid == 0) S.n = 0;
+                __syncthreads();
+                bool ok2[Q + 1];
+#pragma unroll
+                for (int q = 0; q <= Q; ++q)
+                    ok2[q] = okr[q] && (bs >= kPassBins || dbin_key(M, comp_k(xs[q])) <= bs);
+                uint64_t unused = 0;
+                cand_commit(S, xs, ok2, safe, unused, false, M);
+                __syncthreads();
+                nv = (int)S.n;
+                __syncthreads();
+            } else if (narrow && (cnt > 0 || by_mass)) {
                 nv = by_mass ? narrow_binned(S, nv, M, cnt, g) : narrow_candidates(S, nv, M, cnt, false, g);
+            }
 
             sort_desc(S, nv);
             sorted = true;
