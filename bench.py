@@ -74,6 +74,35 @@ def measured_traffic(kernel: str, config: int):
     return None
 
 
+KSCAN_SOURCES = ("scan.h", "common.h", "k_scan.hip")
+
+
+def kscan_sources_hash() -> str:
+    """First 16 hex digits of the sha256 of k_scan's sources, as the committed
+    counter summary records the ones it measured."""
+    import hashlib
+
+    csrc = os.path.join(_REPO, "full-inference-engine_amd", "csrc")
+    h = hashlib.sha256()
+    for name in KSCAN_SOURCES:
+        with open(os.path.join(csrc, name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def traffic_sources(config: int):
+    """The k_scan sources hash the committed FETCH/WRITE summary was measured on."""
+    path = os.path.join(_REPO, "profiles", f"k_scan_C{config}_hbm_traffic.md")
+    try:
+        with open(path, encoding="utf-8") as f:
+            for line in f:
+                if line.startswith("k_scan sources measured") and "`" in line:
+                    return line.split("`")[1]
+    except OSError:
+        pass
+    return None
+
+
 def algorithmic_bytes(w, hp) -> dict:
     """Bytes one step must move at least (one read of the logits), per kernel.
 
@@ -334,6 +363,8 @@ def main() -> None:
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": measured_traffic(dom, a.config),
             "traffic_source": f"profiles/k_scan_C{a.config}_hbm_traffic.md (rocprofv3 --pmc, scaled)",
+            # the summary is of the k_scan sources it names; false: they changed since
+            "traffic_matches_sources": traffic_sources(a.config) == kscan_sources_hash(),
             "algorithmic_bytes": dom_bytes,
         },
         "step_roofline": {"achieved": step_gbs, "frac": step_gbs / HBM_PEAK_GBS,
