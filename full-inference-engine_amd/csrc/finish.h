@@ -230,8 +230,80 @@ FIE_DEV void row_pass(FinSmem& S, const KParams& P, int row, float s, bool pen, 
     if (tid == 0 && k0) f(key_to_float(k0), 0u);
     uint4 buf[D][NL];
     uint32_t bof[D];
+    bool overflow = false;
     if (pen) {
-        for (int i = tid; i < P.NS; i += kFinThreads) S.snb[i] = P.w.nb[(size_t)row * P.NS + i];
+        for (int i = tid; i < P.NS; i += kFinThreads) {
+            const uint32_t nb = P.w.nb[(size_t)row * P.NS + i];
+            S.snb[i] = nb;
+            overflow |= nb > (uint32_t)kBucketCap;
+        }
+    }
+    if (VEC && !__syncthreads_or(overflow)) {
+        // The common case, as straight-line streaming: whole chunks, one vector load
+        // per group, every span's bucket complete.  Every step of the ring issues the
+        // same loads (past the last whole chunk it reloads that chunk, unused), so the
+        // compiler's wait counts see the D - 1 chunks still in flight; the partial
+        // last chunk follows the ring.
+        const int nfull = V / kChunk;
+        auto issue_full = [&](uint4 (&b)[NL], uint32_t& of, int c) {
+            const int lo = (c < nfull ? c : nfull - 1) * kChunk;
+#pragma unroll
+            for (int j = 0; j < NL; ++j) b[j] = *(const uint4*)(rowp + (size_t)(lo + (j * kFinThreads + tid) * EPL) * SZ);
+            of = P.w.bk[((size_t)row * P.NS + lo / kSpan) * kBucketCap + tid];
+        };
+        auto count_bucket = [&](uint32_t of, int lo) {
+            for (int i = tid; i < kChunk / 4; i += kFinThreads) ((uint4*)S.cnt)[i] = make_uint4(0, 0, 0, 0);
+            __syncthreads();
+            const uint32_t o = of - (uint32_t)(lo % kSpan);
+            if ((uint32_t)tid < S.snb[lo / kSpan] && o < (uint32_t)kChunk) atomicAdd(&S.cnt[o], 1u);
+            __syncthreads();
+        };
+        auto visit = [&](const uint4 (&b)[NL], int lo) {
+#pragma unroll
+            for (int j = 0; j < NL; ++j) {
+                const int e0 = lo + (j * kFinThreads + tid) * EPL;
+#pragma unroll
+                for (int e = 0; e < EPL; ++e) {
+                    const int idx = e0 + e;
+                    if (idx >= V || idx == 0) continue;
+                    float x = lane_get<DT>(b[j], e);
+                    if (pen) {
+                        const uint32_t cc = S.cnt[idx - lo];
+                        if (cc) x = penalize(x, rep, pres, freq, cc);
+                    }
+                    float y;
+                    if (s == 1.0f) y = x + 0.0f;
+                    else if (mark && markstein_ok(x)) y = div_markstein(x, s, rs) + 0.0f;
+                    else y = scaled(x, s);
+                    f(y, (uint32_t)idx);
+                }
+            }
+        };
+        if (nfull > 0) {
+#pragma unroll
+            for (int q = 0; q < D; ++q) issue_full(buf[q], bof[q], q);
+            for (int c0 = 0; c0 < nfull; c0 += D) {
+#pragma unroll
+                for (int q = 0; q < D; ++q) {
+                    const int c = c0 + q;
+                    if (c < nfull) {
+                        if (pen) count_bucket(bof[q], c * kChunk);
+                        visit(buf[q], c * kChunk);
+                        if (pen) __syncthreads();
+                    }
+                    issue_full(buf[q], bof[q], c + D);
+                }
+            }
+        }
+        const int lo = nfull * kChunk;
+        if (lo < V) {
+#pragma unroll
+            for (int j = 0; j < NL; ++j) buf[0][j] = load_group<DT, VEC>(rowp, lo + (j * kFinThreads + tid) * EPL, V);
+            if (pen) count_bucket(P.w.bk[((size_t)row * P.NS + lo / kSpan) * kBucketCap + tid], lo);
+            visit(buf[0], lo);
+        }
+        __syncthreads();
+        return;
     }
     auto issue = [&](uint4 (&b)[NL], uint32_t& of, int c) {
         const int lo = c * kChunk;
