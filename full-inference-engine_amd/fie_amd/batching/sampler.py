@@ -82,7 +82,7 @@ class ParamTable:
     identity match cannot be a new object at a recycled address."""
 
     __slots__ = ("objs", "greedy", "pen", "temps", "top_k", "top_p", "min_p", "lp",
-                 "rep", "pres", "freq", "seeded", "seeds")
+                 "rep", "pres", "freq", "seeded", "seeds", "_resolved")
 
     def __init__(self, params: list[SamplingParams]):
         self.objs = list(params)
@@ -103,6 +103,21 @@ class ParamTable:
         self.freq = np.array(cols[9], dtype=np.float32)
         self.seeded = np.array(cols[10], dtype=bool)
         self.seeds = np.array(cols[11], dtype=np.uint64) if rows else np.zeros(0, np.uint64)
+        self._resolved: dict[int, tuple] = {}
+
+    def resolved(self, vocab: int) -> tuple:
+        """(scale, top_k, top_p, min_p, flags) as the kernels take them, resolved the way
+        sampler.py:182-192 does for this vocabulary (computed once per table)."""
+        r = self._resolved.get(vocab)
+        if r is None:
+            greedy, pen = self.greedy, self.pen
+            r = (np.where(greedy, 1.0, self.temps).astype(np.float32),
+                 np.where((self.top_k > 0) & (self.top_k < vocab) & ~greedy, self.top_k, 0).astype(np.int32),
+                 np.where((self.top_p < 1.0) & ~greedy, self.top_p, 1.0).astype(np.float32),
+                 np.where((self.min_p > 0.0) & ~greedy, self.min_p, 0.0).astype(np.float32),
+                 greedy.astype(np.int32) * FLAG_GREEDY + pen.astype(np.int32) * FLAG_PENALTY)
+            self._resolved[vocab] = r
+        return r
 
     def matches(self, params: list[SamplingParams]) -> bool:
         objs = self.objs
@@ -143,12 +158,13 @@ def resolve_params(params: list[SamplingParams], vocab: int, uniforms: np.ndarra
         offsets, ids, invalid, longest = pack_history(contexts, pen, vocab)
     else:
         offsets, ids, invalid, longest = np.zeros(rows + 1, np.int64), _EMPTY.astype(np.int32), None, 0
+    r_scale, r_top_k, r_top_p, r_min_p, r_flags = t.resolved(vocab)
     return HostParams(
-        scale=np.where(greedy, 1.0, temps).astype(np.float32),
-        top_k=np.where((top_k > 0) & (top_k < vocab) & ~greedy, top_k, 0).astype(np.int32),
-        top_p=np.where((top_p < 1.0) & ~greedy, top_p, 1.0).astype(np.float32),
-        min_p=np.where((min_p > 0.0) & ~greedy, min_p, 0.0).astype(np.float32),
-        flags=(greedy.astype(np.int32) * FLAG_GREEDY + pen.astype(np.int32) * FLAG_PENALTY),
+        scale=r_scale,
+        top_k=r_top_k,
+        top_p=r_top_p,
+        min_p=r_min_p,
+        flags=r_flags,
         logprobs=t.lp,
         uniform=np.ascontiguousarray(uniforms, dtype=np.float64),
         rep=t.rep,
