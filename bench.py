@@ -188,6 +188,47 @@ def time_config(config: int, steps: int, warmup: int, ring_mb: int, dev):
     }
 
 
+def full_row_us(dev, steps: int = 50) -> dict:
+    """Step latency when rows need the full-row path (the draw lies past the streamed
+    candidates): C1's plain rows (N(0, 3^2) fp32 logits, temperature 1) with draws
+    deep in the tail, one row alone and the four together."""
+    import numpy as np
+    import torch
+
+    from fie_amd import _lib
+    from fie_amd import workloads as W
+    from fie_amd.batching.sampler import resolve_params
+    from fie_amd.kernel import FusedSampler
+
+    w = W.make(1)
+    fs = FusedSampler(dev)
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for name, rows in (("one_row", [4]), ("four_rows", [4, 5, 6, 7])):
+        x = w.logits[rows].to(dev)
+        params = [w.params[r] for r in rows]
+        u = np.array([0.95, 0.96, 0.97, 0.98])[:len(rows)]
+        hp = resolve_params(params, x.shape[1], u, None)
+        buf = fs.step_buffers(len(rows), 0)
+        buf.stage(hp)
+        buf.upload(stream)
+        args = fs.build_args(x, buf, hp)
+        for _ in range(5):
+            fs.launch(args)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fs.launch(args)
+        e1.record(stream)
+        buf.download(stream)
+        torch.cuda.synchronize()
+        out = buf.outputs()
+        res[name] = {"us_per_step": e0.elapsed_time(e1) / steps * 1e3,
+                     "exact_path_rows": int((out["status"] & _lib.FIE_ROW_EXACT_PATH != 0).sum())}
+    return res
+
+
 def end_to_end_ms(w, dev, reps: int = 20) -> float:
     """BatchedSampler.sample() as the engine calls it, per decode step: parameter
     resolution, the appended context token per row (the contexts stay on the
@@ -389,6 +430,10 @@ def main() -> None:
         del r
         torch.cuda.empty_cache()
     line["other_configs"] = others
+    try:
+        line["full_row_path"] = full_row_us(dev)
+    except Exception as e:  # report, never hide the main line
+        line["full_row_path"] = f"failed: {e}"
     if a.lmhead_dim:
         try:
             line["lmhead_fused"] = time_lmhead(w, dev, a.lmhead_dim)

@@ -615,20 +615,53 @@ template <int DT, bool VEC>
 FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pen, float rep,
                          float pres, float freq, uint32_t k0, float M, int topk, float mp, float tp,
                          double u, u128 sall, uint32_t* tk_out, uint32_t* tau_out, uint64_t* cut_out,
-                         u128* T_out, uint64_t* tok_out)
+                         u128* T_out, uint64_t* tok_out, bool hd)
 {
     const int tid = threadIdx.x;
-    for (int i = tid; i < kPassBins; i += kFinThreads) {
-        S.pc[i] = 0;
-        S.pm_lo[i] = 0;
-        S.pm_hi[i] = 0;
+    // The span helpers' histograms and bucketed composites stand in for the passes
+    // when every helper binned against this row maximum (token 0 is not the
+    // maximum); otherwise the row is re-read.
+    bool use_h = false;
+    if (hd) {
+        bool ok = true;
+        for (int i = tid; i < P.NS; i += kFinThreads) ok &= P.w.hmk[(size_t)row * P.NS + i] == fkey(M);
+        use_h = __syncthreads_and(ok);
     }
-    __syncthreads();
-    row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](float y, uint32_t idx) {
-        const int b = dbin_y(M, y);
-        atomicAdd(&S.pc[b], 1u);
-        bin_add(S, b, weight_of(S, y, idx));
-    });
+    if (use_h) {
+        for (int b = tid; b < kPassBins; b += kFinThreads) {
+            uint32_t c = 0;
+            uint64_t lo = 0, hi = 0;
+            for (int sp = 0; sp < P.NS; ++sp) {
+                const size_t o = ((size_t)row * P.NS + sp) * kHBins + b;
+                c += P.w.hpc[o];
+                lo += P.w.hlo[o];
+                hi += P.w.hhi[o];
+            }
+            S.pc[b] = c;
+            S.pm_lo[b] = lo;
+            S.pm_hi[b] = hi;
+        }
+        __syncthreads();
+        if (tid == 0 && k0) {
+            const float y = key_to_float(k0);
+            const int b = dbin_y(M, y);
+            S.pc[b] += 1u;
+            bin_add(S, b, weight_of(S, y, 0u));
+        }
+        __syncthreads();
+    } else {
+        for (int i = tid; i < kPassBins; i += kFinThreads) {
+            S.pc[i] = 0;
+            S.pm_lo[i] = 0;
+            S.pm_hi[i] = 0;
+        }
+        __syncthreads();
+        row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](float y, uint32_t idx) {
+            const int b = dbin_y(M, y);
+            atomicAdd(&S.pc[b], 1u);
+            bin_add(S, b, weight_of(S, y, idx));
+        });
+    }
     // S.cand holds the elements (ncur of them) of bins [cur_lo, cur_hi] and, when
     // cur2_lo >= 0, of bins [cur2_lo, cur2_hi] as well.
     int cur_lo = -1, cur_hi = -1, cur2_lo = -1, cur2_hi = -1, ncur = 0;
@@ -638,6 +671,47 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
         for (int b = bl; b <= bh; ++b) cnt += S.pc[b];
         for (int b = b2l; b2l >= 0 && b <= b2h; ++b) cnt += S.pc[b];
         if (cnt > (uint32_t)kGCap) return false;
+        if (use_h) {
+            // the bins' segments of every span's bucketed composites, concatenated
+            __syncthreads();
+            const int nseg = 2 * P.NS;
+            uint32_t st = 0, len = 0;
+            if (tid < nseg) {
+                const int sp = tid >> 1, l = (tid & 1) ? b2l : bl, h = (tid & 1) ? b2h : bh;
+                if (l >= 0) {
+                    const uint32_t* off = P.w.hoff + ((size_t)row * P.NS + sp) * kHOffs;
+                    st = off[l];
+                    len = off[h + 1] - st;
+                }
+            }
+            uint32_t total;
+            const uint32_t pre = block_excl_scan_u32<kFinThreads>(len, S.red32, &total);
+            if (tid < nseg) {
+                S.hc[tid] = pre;
+                S.cnt[tid] = st;
+            }
+            __syncthreads();
+            const uint32_t n = total < (uint32_t)kGCap ? total : (uint32_t)kGCap;
+            for (uint32_t i = tid; i < n; i += kFinThreads) {
+                int lo = 0, hi = nseg - 1;            // the last segment starting at or before i
+                while (lo < hi) {
+                    const int mid = (lo + hi + 1) >> 1;
+                    if (S.hc[mid] <= i) lo = mid;
+                    else hi = mid - 1;
+                }
+                const size_t src = ((size_t)row * P.NS + (lo >> 1)) * kSpan + S.cnt[lo] + (i - S.hc[lo]);
+                S.cand[i] = P.w.hcomp[src];
+            }
+            uint32_t m = n;
+            if (k0) {
+                const int b = dbin_y(M, key_to_float(k0));
+                if (((b >= bl && b <= bh) || (b2l >= 0 && b >= b2l && b <= b2h)) && m < (uint32_t)kGCap) {
+                    if (tid == 0) S.cand[m] = comp_key(k0, 0);
+                    ++m;
+                }
+            }
+            ncur = (int)m;
+        } else {
         if (tid == 0) S.n = 0;
         __syncthreads();
         row_pass<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, [&](float y, uint32_t idx) {
@@ -648,6 +722,7 @@ FIE_DEV bool binned_deep(FinSmem& S, const KParams& P, int row, float s, bool pe
             }
         });
         ncur = (int)S.n;
+        }
         cur_lo = bl;
         cur_hi = bh;
         cur2_lo = b2l;
@@ -1307,7 +1382,7 @@ FIE_DEV void sorted_find(FinSmem& S, const SortedScan& sc, u128 g, int* slot_i, 
 // phases compute the same prologue (row maximum, tile table, row mass) from the
 // partials; a queued row's DeferRec carries what PH 1 cannot recompute cheaply.
 template <int DT, bool VEC, int PH, int Q>
-FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool inl)
+FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool inl, const bool hd = false)
 {
     const fie_sampler_args& a = P.a;
     const int tid = threadIdx.x, NT = P.NT;
@@ -1640,7 +1715,7 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
         cut = 0;
         uint32_t tk = 0;
         const bool binned = binned_deep<DT, VEC>(S, P, row, s, pen, rep, pres, freq, k0, M, topk, mp, tp,
-                                                 urow, sall, &tk, &tau, &cut, &T, &tok_comp);
+                                                 urow, sall, &tk, &tau, &cut, &T, &tok_comp, hd);
         if (!binned) {
         // radix levels over the composite, re-reading the row per level
         cut = 0;
@@ -1767,6 +1842,208 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
     }
 }
 
+// ---------------------------------------------------------------- span helpers
+// Batches of at most kHelpRows rows leave most CUs idle, and a row the candidates
+// cannot settle would stream all of its tokens through one workgroup.  There,
+// k_finish runs one helper workgroup per span of each sampled row beside the
+// row's own workgroup.  A helper bins its span's tokens by d = fl(M - y) exactly as
+// the full-row pass does (counts and R1 masses per bin) and stores the span's
+// composites ordered by bin, so the full-row selection reads one histogram per
+// span and gathers a bin from the spans' segments instead of re-reading the row.
+// Nobody waits: each of the row's workgroups counts itself in (harr) after its
+// stores, and the last to arrive finishes the row if its own workgroup handed it
+// to the full-row path.  Rows with a small top-k never take that path.
+constexpr int kHelpTopK = 1024;
+static_assert(kHBins == kPassBins && kHBins == 2 * kFinThreads, "two bins per thread");
+
+FIE_DEV bool helped_row(const KParams& P, int row)
+{
+    if (P.a.flags[row] & FIE_FLAG_GREEDY) return false;
+    const int k = P.a.top_k[row];
+    return k == 0 || k > kHelpTopK;
+}
+
+// Counts the workgroup in at the row; true for the last of its NS + 1 workgroups,
+// which then sees every other one's stores.  Every wave waits for its own stores to
+// complete, then one thread fences for the workgroup: a device-scope fence per wave
+// costs ~0.2 us each, serialised across the helpers.
+FIE_DEV bool arrive(FinSmem& S, const KParams& P, int row)
+{
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        __threadfence();
+        const uint32_t n = atomicAdd(&P.w.harr[row], 1u);
+        const bool last = n == (uint32_t)P.NS;
+        if (last) {
+            P.w.harr[row] = 0u;              // ready for the next call
+            __threadfence();
+        }
+        S.ibin = last ? 1 : 0;
+    }
+    __syncthreads();
+    const bool last = S.ibin != 0;
+    __syncthreads();
+    return last;
+}
+
+// Returns true when this workgroup is to finish the row through the full-row path.
+template <int DT, bool VEC>
+FIE_DEV bool span_helper(FinSmem& S, const KParams& P, const int row, const int sp)
+{
+    constexpr int EPL = DTy<DT>::EPL, SZ = DTy<DT>::SZ;
+    constexpr int NL = kSpan / kFinThreads / EPL;
+    const fie_sampler_args& a = P.a;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int NT = P.NT, NS = P.NS, V = a.vocab;
+    if (!helped_row(P, row)) return false;
+    const int32_t fl = a.flags[row];
+    const bool pen = a.apply_penalties && (fl & FIE_FLAG_PENALTY);
+    const float s = a.scale[row];
+    float rep = 1.0f, pres = 0.0f, freq = 0.0f;
+    if (pen) { rep = a.repetition[row]; pres = a.presence[row]; freq = a.frequency[row]; }
+    const int lo = sp * kSpan;
+    const char* rowp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * SZ;
+    uint4 raw[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) raw[j] = load_group<DT, VEC>(rowp, lo + (j * kFinThreads + tid) * EPL, V);
+    const uint64_t pf_max = tid < NT ? P.w.maxc[(size_t)row * NT + tid] : 0ull;
+    const size_t hs = (size_t)row * NS + sp;
+    uint32_t nb = 0, of = 0;
+    if (pen) {
+        nb = P.w.nb[hs];
+        of = P.w.bk[hs * kBucketCap + tid];
+    }
+    uint32_t* cnt = (uint32_t*)S.cand;       // penalty counts of the span's tokens
+    for (int i = tid; i < kPassBins; i += kFinThreads) {
+        S.pc[i] = 0;
+        S.pm_lo[i] = 0;
+        S.pm_hi[i] = 0;
+    }
+    if (pen)
+        for (int i = tid; i < kSpan / 4; i += kFinThreads) ((uint4*)cnt)[i] = make_uint4(0, 0, 0, 0);
+    {
+        const uint64_t wm = wave_max_u64(pf_max);
+        if (lane == 0) S.red64[wave] = wm;
+    }
+    __syncthreads();
+    // the row maximum and the span's tiles of the R1 tile table, as the row's own
+    // workgroup computes them (token 0 left out: the row's workgroup checks it)
+    uint64_t xm = 0;
+    for (int w = 0; w < kFinWaves; ++w) xm = S.red64[w] > xm ? S.red64[w] : xm;
+    const uint32_t kxm = xm ? fkey(y_of_xkey(comp_k(xm), s)) : 0u;
+    const float M = key_to_float(kxm);
+    if (tid < NT && tid / kWavesPerWG == sp) {
+        const float mt = pf_max ? y_of_xkey(comp_k(pf_max), s) : 0.0f;
+        S.mt[tid + 1] = mt;
+        S.ct[tid + 1] = pf_max ? fixed40(cexp(mt - M)) : 0ull;
+    }
+    if (pen) {
+        if (nb <= (uint32_t)kBucketCap) {
+            if ((uint32_t)tid < nb) atomicAdd(&cnt[of], 1u);
+        } else {
+            const int64_t h0 = a.hist_offsets[row], h1 = hist_end(a, row);
+            const int hi = min(lo + kSpan, V);
+            for (int64_t h = h0 + tid; h < h1; h += kFinThreads) {
+                const uint32_t id = (uint32_t)a.hist_ids[h];
+                if (id >= (uint32_t)lo && id < (uint32_t)hi && id != 0) atomicAdd(&cnt[id - lo], 1u);
+            }
+        }
+    }
+    __syncthreads();
+    // every token of the span: its bin, count and mass (row_pass's arithmetic)
+    const bool mark = s != 1.0f && s >= 0x1p-30f && s <= 0x1p30f;
+    const float rs = 1.0f / s;
+    uint64_t cv[NL * EPL];
+    int bv[NL * EPL];
+    // the last bin (d >= 16 and NaN) holds most tokens of a flat or long-tailed row:
+    // summed per thread and per wave first, not by same-address LDS atomics
+    uint32_t tail_n = 0;
+    u128 tail_w = 0;
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const int k = j * EPL + e;
+            const int idx = lo + (j * kFinThreads + tid) * EPL + e;
+            bv[k] = -1;
+            cv[k] = 0;
+            if (idx >= V || idx == 0) continue;
+            float x = lane_get<DT>(raw[j], e);
+            if (pen) {
+                const uint32_t cc = cnt[idx - lo];
+                if (cc) x = penalize(x, rep, pres, freq, cc);
+            }
+            float y;
+            if (s == 1.0f) y = x + 0.0f;
+            else if (mark && markstein_ok(x)) y = div_markstein(x, s, rs) + 0.0f;
+            else y = scaled(x, s);
+            const int b = dbin_y(M, y);
+            const u128 w = weight_of(S, y, (uint32_t)idx);
+            if (b == kPassBins - 1) {
+                ++tail_n;
+                tail_w += w;
+            } else {
+                atomicAdd(&S.pc[b], 1u);
+                bin_add(S, b, w);
+            }
+            bv[k] = b;
+            cv[k] = comp_key(fkey(y), (uint32_t)idx);
+        }
+    }
+    tail_n = wave_sum_u32(tail_n);
+    tail_w = wave_sum_u128(tail_w);
+    if (lane == 0 && tail_n) {
+        atomicAdd(&S.pc[kPassBins - 1], tail_n);
+        bin_add(S, kPassBins - 1, tail_w);
+    }
+    __syncthreads();
+    // the histogram and the bins' offsets, then the composites in bin order
+    const uint32_t ca = S.pc[2 * tid], cb = S.pc[2 * tid + 1];
+    {
+        const size_t o = hs * kHBins + 2 * tid;
+        P.w.hpc[o] = ca;
+        P.w.hpc[o + 1] = cb;
+        P.w.hlo[o] = S.pm_lo[2 * tid];
+        P.w.hlo[o + 1] = S.pm_lo[2 * tid + 1];
+        P.w.hhi[o] = S.pm_hi[2 * tid];
+        P.w.hhi[o + 1] = S.pm_hi[2 * tid + 1];
+    }
+    uint32_t total;
+    const uint32_t ex = block_excl_scan_u32<kFinThreads>(ca + cb, S.red32, &total);
+    S.cnt[2 * tid] = ex;
+    S.cnt[2 * tid + 1] = ex + ca;
+    {
+        uint32_t* off = P.w.hoff + hs * kHOffs;
+        off[2 * tid] = ex;
+        off[2 * tid + 1] = ex + ca;
+        if (tid == 0) {
+            off[kHBins] = total;
+            P.w.hmk[hs] = fkey(M);
+        }
+    }
+    __syncthreads();
+    const uint64_t below = lane ? (~0ull >> (64 - lane)) : 0ull;   // lanes before this one
+#pragma unroll
+    for (int k = 0; k < NL * EPL; ++k) {
+        const bool tail = bv[k] == kPassBins - 1;
+        const uint64_t m = __ballot(tail);
+        if (m) {
+            // the last bin's slots: one LDS atomic per wave, ranks by lane
+            const int first = __ffsll((unsigned long long)m) - 1;
+            uint32_t base = 0;
+            if (lane == first) base = atomicAdd(&S.cnt[kPassBins - 1], (uint32_t)__popcll(m));
+            base = (uint32_t)__shfl((int)base, first);
+            if (tail) P.w.hcomp[hs * kSpan + base + (uint32_t)__popcll(m & below)] = cv[k];
+        }
+        if (bv[k] >= 0 && !tail) {
+            const uint32_t at = atomicAdd(&S.cnt[bv[k]], 1u);
+            P.w.hcomp[hs * kSpan + at] = cv[k];
+        }
+    }
+    return arrive(S, P, row) && P.w.dfr[row].mode != 0;
+}
+
 // One workgroup per row.  A row's finish is a chain of dependent steps, so its
 // latency is the kernel's: with no more rows than CUs (one workgroup each) the WIDE
 // variant takes up to 256 registers a lane and spills nothing; larger batches take
@@ -1775,11 +2052,31 @@ template <int DT, bool VEC, bool WIDE>
 __global__ __launch_bounds__(kFinThreads, WIDE ? 2 : 4) void k_finish(const KParams P)
 {
     __shared__ FinSmem S;
-    finish_row<DT, VEC, 0, WIDE ? 10 : kReloadQ>(S, P, blockIdx.x, WIDE);
     if constexpr (WIDE) {
-        // a row the candidates could not settle takes the full-row path here, at once
-        __syncthreads();
-        if (S.dmode) finish_row<DT, VEC, 1, kReloadQ>(S, P, blockIdx.x, true);
+        // a row the candidates could not settle takes the full-row path here, at once;
+        // with span helpers, in whichever of the row's workgroups arrives last
+        bool deep, inl = true, hd = false;
+        if (blockIdx.y > 0) {
+            deep = span_helper<DT, VEC>(S, P, blockIdx.x, blockIdx.y - 1);
+            inl = false;
+            hd = true;
+        } else {
+            finish_row<DT, VEC, 0, 10>(S, P, blockIdx.x, true);
+            __syncthreads();
+            deep = S.dmode != 0;
+            if (P.helpers && helped_row(P, blockIdx.x)) {
+                if (threadIdx.x == 0) {
+                    DeferRec d = S.dfr;
+                    if (!deep) d.mode = 0;
+                    P.w.dfr[blockIdx.x] = d;
+                }
+                deep = arrive(S, P, blockIdx.x) && deep;
+                hd = true;
+            }
+        }
+        if (deep) finish_row<DT, VEC, 1, kReloadQ>(S, P, blockIdx.x, inl, hd);
+    } else {
+        finish_row<DT, VEC, 0, kReloadQ>(S, P, blockIdx.x, false);
     }
 }
 

@@ -11,10 +11,10 @@ hipError_t launch_finish_f16(const KParams& P, bool vec, bool deep, bool wide, h
         if (vec) k_deep<FIE_F16, true><<<P.a.rows, kFinThreads, 0, st>>>(P);
         else k_deep<FIE_F16, false><<<P.a.rows, kFinThreads, 0, st>>>(P);
     } else if (vec) {
-        if (wide) k_finish<FIE_F16, true, true><<<P.a.rows, kFinThreads, 0, st>>>(P);
+        if (wide) k_finish<FIE_F16, true, true><<<dim3(P.a.rows, P.helpers ? P.NS + 1 : 1), kFinThreads, 0, st>>>(P);
         else k_finish<FIE_F16, true, false><<<P.a.rows, kFinThreads, 0, st>>>(P);
     } else {
-        if (wide) k_finish<FIE_F16, false, true><<<P.a.rows, kFinThreads, 0, st>>>(P);
+        if (wide) k_finish<FIE_F16, false, true><<<dim3(P.a.rows, P.helpers ? P.NS + 1 : 1), kFinThreads, 0, st>>>(P);
         else k_finish<FIE_F16, false, false><<<P.a.rows, kFinThreads, 0, st>>>(P);
     }
     return hipGetLastError();

@@ -121,6 +121,7 @@ __global__ __launch_bounds__(kLhThreads, 4) void k_lmhead(const KParams P, const
     const int tile = 8 * (k / nrb) + xcd, rb = k % nrb;
     if (tile >= NT) return;
     if (blockIdx.x == 0 && tid < 2) P.w.dq[tid] = 0u;   // k_deep's queue, filled by k_finish
+    if (P.helpers && blockIdx.x == 0 && tid < B) P.w.harr[tid] = 0u;   // k_finish's arrivals
     const int r0 = rb * kLhRows;
     const int64_t ld = a.row_stride;
     uint16_t* out = (uint16_t*)a.logits;

@@ -214,7 +214,9 @@ static int fail(int code, const char* msg)
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct Layout {
-    size_t maxc, sw, bound, ncand, nu, nb, bk, cand, tok0x, tok0c, bad, res, mt, ct, dq, dqrows, dfr, total;
+    size_t maxc, sw, bound, ncand, nu, nb, bk, cand, tok0x, tok0c, bad, res, mt, ct, dq, dqrows, dfr;
+    size_t harr, hmk, hpc, hlo, hhi, hoff, hcomp;   // span helpers (0: none)
+    size_t total;
 };
 
 static bool layout_of(int32_t R, int32_t V, Layout* L)
@@ -242,6 +244,17 @@ static bool layout_of(int32_t R, int32_t V, Layout* L)
     L->dq = take(2 * 4);
     L->dqrows = take(r * 4);
     L->dfr = take(r * sizeof(DeferRec));
+    // span helpers of k_finish: only workspaces for at most kHelpRows rows hold them
+    L->harr = L->hmk = L->hpc = L->hlo = L->hhi = L->hoff = L->hcomp = 0;
+    if (R <= kHelpRows) {
+        L->harr = take(r * 4);
+        L->hmk = take(r * NS * 4);
+        L->hpc = take(r * NS * kHBins * 4);
+        L->hlo = take(r * NS * kHBins * 8);
+        L->hhi = take(r * NS * kHBins * 8);
+        L->hoff = take(r * NS * kHOffs * 4);
+        L->hcomp = take(r * NS * kSpan * 8);
+    }
     L->total = o;
     return true;
 }
@@ -275,6 +288,14 @@ static int ws_of(const fie_workspace* ws, int32_t rows, int32_t V, Ws* w)
     w->dq = (uint32_t*)(b + L.dq);
     w->dqrows = (uint32_t*)(b + L.dqrows);
     w->dfr = (DeferRec*)(b + L.dfr);
+    const bool h = L.harr != 0;
+    w->harr = h ? (uint32_t*)(b + L.harr) : nullptr;
+    w->hmk = h ? (uint32_t*)(b + L.hmk) : nullptr;
+    w->hpc = h ? (uint32_t*)(b + L.hpc) : nullptr;
+    w->hlo = h ? (uint64_t*)(b + L.hlo) : nullptr;
+    w->hhi = h ? (uint64_t*)(b + L.hhi) : nullptr;
+    w->hoff = h ? (uint32_t*)(b + L.hoff) : nullptr;
+    w->hcomp = h ? (uint64_t*)(b + L.hcomp) : nullptr;
     return FIE_OK;
 }
 
@@ -374,8 +395,14 @@ static int prepare(const fie_sampler_args* args, const fie_workspace* ws, KParam
     P->a = *args;
     P->NT = (args->vocab + kTile - 1) / kTile;
     P->NS = (P->NT + kWavesPerWG - 1) / kWavesPerWG;
+    P->helpers = 0;
     if (args->rows == 0) return FIE_OK;
-    return ws_of(ws, args->rows, args->vocab, &P->w);
+    rc = ws_of(ws, args->rows, args->vocab, &P->w);
+    if (rc != FIE_OK) return rc;
+    // small batches, settled in place by the wide k_finish, in a workspace that
+    // holds the helpers' arrays
+    P->helpers = (P->w.harr && args->rows <= kHelpRows && finish_in_place(*P)) ? 1 : 0;
+    return FIE_OK;
 }
 
 // ---------------------------------------------------------------- static scratch

@@ -35,7 +35,10 @@ constexpr int kMaxTiles = 256;                   // vocab <= 256 * 2048
 constexpr int kBucketCap = 512;                  // history ids of one span held by k_prep
 constexpr int kMaxSpans = kMaxTiles / kWavesPerWG;
 constexpr int kPrepThreads = 256;
-constexpr int kPS = 4;                           // penalised tokens per lane held in slots
+constexpr int kPS = 4;
+constexpr int kHelpRows = 16;                    // batches up to this many rows get span helpers
+constexpr int kHBins = 1024;                     // d-bins of a helper's histogram
+constexpr int kHOffs = kHBins + 4;               // bin offsets per helper (kHBins + 1, padded)                           // penalised tokens per lane held in slots
 
 // Result of one row kept for fie_sampler_kept().
 struct RowRes {
@@ -77,6 +80,17 @@ struct Ws {
     uint32_t* dq;        // [2] rows queued for k_deep, and taken; k_scan clears both
     uint32_t* dqrows;    // [rows] the queued rows
     DeferRec* dfr;       // [rows]
+    // Span helpers of k_finish (batches of at most kHelpRows rows; NULL otherwise),
+    // per (row, span): the span's d-bin histogram (counts and the two 41-bit mass
+    // limbs), the bins' offsets and the span's composites in bin order, and the
+    // row-maximum key the helper binned against.
+    uint32_t* harr;      // [rows] arrivals at a row (helpers and its finishing workgroup)
+    uint32_t* hmk;       // [rows * NS]
+    uint32_t* hpc;       // [rows * NS * kHBins]
+    uint64_t* hlo;       // [rows * NS * kHBins]
+    uint64_t* hhi;       // [rows * NS * kHBins]
+    uint32_t* hoff;      // [rows * NS * kHOffs]
+    uint64_t* hcomp;     // [rows * NS * kSpan]
 };
 
 struct KParams {
@@ -84,6 +98,7 @@ struct KParams {
     Ws w;
     int NT;
     int NS;              // spans of kSpan tokens per row
+    int helpers;         // 1: k_finish runs one helper workgroup per span of each sampled row
 };
 
 // ---------------------------------------------------------------- element access
@@ -583,6 +598,7 @@ __global__ __launch_bounds__(kScanThreads) void k_scan(const KParams P)
     const char* rowp = (const char*)a.logits + (size_t)row * (size_t)a.row_stride * SZ;
     const size_t slot = (size_t)row * NT + tile;
     if (blockIdx.x == 0 && blockIdx.y == 0 && tid < 2) P.w.dq[tid] = 0u;   // k_deep's queue, filled by k_finish
+    if (P.helpers && blockIdx.x == 0 && tid == 0) P.w.harr[row] = 0u;     // k_finish's arrivals at the row
 
     // 1. The span's history bucket (k_prep), then every load of the tile: the
     //    history is counted while the logits are in flight.

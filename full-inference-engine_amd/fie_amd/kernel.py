@@ -41,6 +41,9 @@ _TABLE_FIELDS = frozenset(("scale", "top_k", "top_p", "min_p", "flags", "logprob
 
 FLAG_GREEDY = _lib.FIE_FLAG_GREEDY
 FLAG_PENALTY = _lib.FIE_FLAG_PENALTY
+# Batches of at most this many rows run k_finish's span helpers, in a workspace
+# sized for exactly this many rows (kHelpRows in the library).
+HELP_ROWS = 16
 
 
 def _align(x: int, a: int = 256) -> int:
@@ -191,25 +194,30 @@ class FusedSampler:
                 "the MI355X sampler runs on a HIP device; got device "
                 f"{self.device} (there is no CPU path)")
         self.lib = _lib.load()
-        self._ws_tensor: torch.Tensor | None = None
-        self._ws = Workspace()
-        self._ws_dims = (0, 0)
+        # Two workspaces: batches of at most HELP_ROWS rows use one sized for
+        # HELP_ROWS, which also holds the span helpers' arrays (the library runs
+        # k_finish's helpers only in such a workspace); larger batches use one that
+        # grows with the largest batch seen.
+        self._wss: dict[bool, tuple[torch.Tensor | None, Workspace, tuple[int, int]]] = {
+            True: (None, Workspace(), (0, 0)), False: (None, Workspace(), (0, 0))}
         self._steps: dict[tuple[int, int], DeviceStep] = {}
 
     # ------------------------------------------------------------------ workspace
     def ensure_workspace(self, rows: int, vocab: int) -> Workspace:
-        r0, v0 = self._ws_dims
+        small = rows <= HELP_ROWS
+        tensor, ws, (r0, v0) = self._wss[small]
         if rows <= r0 and vocab <= v0:
-            return self._ws
-        rows, vocab = max(rows, r0, 1), max(vocab, v0)
+            return ws
+        rows = HELP_ROWS if small else max(rows, r0, 1)
+        vocab = max(vocab, v0)
         nbytes = int(self.lib.fie_sampler_workspace_size(rows, vocab))
         if nbytes == 0:
             raise ValueError(f"unsupported sampler shape rows={rows} vocab={vocab} "
                              f"(vocab must be in [1, {_lib.MAX_VOCAB}])")
-        self._ws_tensor = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
-        self._ws = Workspace(self._ws_tensor.data_ptr(), nbytes, rows, vocab)
-        self._ws_dims = (rows, vocab)
-        return self._ws
+        tensor = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        ws = Workspace(tensor.data_ptr(), nbytes, rows, vocab)
+        self._wss[small] = (tensor, ws, (rows, vocab))
+        return ws
 
     def _stream_ptr(self) -> int:
         return torch.cuda.current_stream(self.device).cuda_stream
@@ -282,7 +290,7 @@ class FusedSampler:
             if want_probs else None
         rc = self.lib.fie_sampler_kept(ctypes.byref(args), kept.data_ptr(),
                                        probs.data_ptr() if probs is not None else None,
-                                       ctypes.byref(self._ws), self._stream_ptr())
+                                       ctypes.byref(self.ensure_workspace(rows, vocab)), self._stream_ptr())
         _lib.check(rc, "fie_sampler_kept")
         return kept, probs
 

@@ -133,7 +133,10 @@ typedef struct fie_workspace {
 } fie_workspace;
 
 /* Bytes of workspace for calls with at most `max_rows` rows and a vocabulary of at
-   most `vocab` (0 on invalid sizes). */
+   most `vocab` (0 on invalid sizes).  A workspace for at most 16 rows also holds the
+   arrays of the per-row kernel's span helpers (about 1.7 MiB a row at vocab 151936):
+   calls of at most 16 rows in such a workspace settle rows the candidates cannot
+   settle with one extra workgroup per 8192-token span of each sampled row. */
 size_t fie_sampler_workspace_size(int32_t max_rows, int32_t vocab);
 
 /* One sampler step: sampler.py:81-117 minus host bookkeeping.  Up to four kernels:

@@ -551,3 +551,72 @@ def test_queued_full_row_rows_match_the_oracle(fs, dtype):
     out, ref, _, _ = run_both(fs, x, params, rng.random(rows), ctx, kept=False)
     check(out, ref, params)
     assert ((out["status"] & 1) != 0).sum() >= rows // 2, "the flat rows should take the full-row path"
+
+
+def _helper_rows(rng, rows, vocab, dtype, sigma=3.0):
+    x = torch.from_numpy(rng.normal(0, sigma, (rows, vocab)).astype(np.float32)).to(dtype)
+    params = [SamplingParams(temperature=1.0),
+              SamplingParams(temperature=1.0, top_p=0.9),
+              SamplingParams(temperature=0.8, top_p=0.99, repetition_penalty=1.3,
+                             frequency_penalty=0.2, presence_penalty=0.1),
+              SamplingParams(temperature=1.0, min_p=0.001),
+              SamplingParams(temperature=1.0, top_k=5000, top_p=0.95),
+              SamplingParams(),
+              SamplingParams(temperature=1.0, top_k=40),
+              SamplingParams(temperature=1.2, logprobs=4)][:rows]
+    ctx = [rng.integers(0, vocab, 3000).tolist() for _ in range(rows)]
+    ctx[2] += list(range(8192, 9000)) * 2          # a span bucket that overflows
+    return x, params, ctx
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_span_helpers_settle_small_batches(fs, dtype):
+    """Batches of at most 16 rows run k_finish with a helper workgroup per span of
+    each sampled row; the full-row rows (deep draws, deep nuclei, low min-p) are
+    settled from the helpers' histograms and bucketed composites.  Bit-exact with the
+    oracle, twice in a row (the arrival counters reset themselves), and equal to the
+    same rows batched past the helper limit."""
+    rng = np.random.default_rng(11)
+    vocab = 151936
+    x, params, ctx = _helper_rows(rng, 8, vocab, dtype)
+    u = np.array([0.97, 0.5, 0.93, 0.99, 0.9, 0.0, 0.3, 0.95])
+    out, ref, gk, gp = run_both(fs, x, params, u, ctx)
+    assert (out["status"] & _lib.FIE_ROW_EXACT_PATH).sum() >= 3
+    check(out, ref, params, gk, gp, lp=True)
+    again, _, _ = fs.step(x.to(DEV), resolve_params(params, vocab, u, ctx))
+    for key in ("status", "tokens", "cut_comp", "kept_mass", "row_mass", "tk_key"):
+        np.testing.assert_array_equal(again[key], out[key], err_msg=key)
+    rep = 3                                                   # 24 rows: no helpers
+    print(f"  case: the same rows x{rep} (past the helper limit)", flush=True)
+    many, _, _ = fs.step(x.repeat(rep, 1).to(DEV), resolve_params(params * rep, vocab, np.tile(u, rep), ctx * rep))
+    for key in ("status", "tokens", "cut_comp", "kept_mass", "row_mass", "tk_key"):
+        np.testing.assert_array_equal(many[key], np.concatenate([out[key]] * rep), err_msg=key)
+
+
+def test_span_helpers_lone_rows_and_odd_shapes(fs):
+    """One deep row alone; an unaligned row stride (scalar loads); a vocabulary that
+    ends inside a span; token 0 as the row maximum (the helpers' maximum leaves it
+    out, so the row is re-read instead)."""
+    rng = np.random.default_rng(12)
+    x = torch.from_numpy(rng.normal(0, 3.0, (1, 151936)).astype(np.float32))
+    p = [SamplingParams(temperature=1.0, top_p=0.95)]
+    out, ref, gk, gp = run_both(fs, x, p, np.array([0.98]))
+    assert out["status"][0] & _lib.FIE_ROW_EXACT_PATH
+    check(out, ref, p, gk, gp)
+    for vocab in (20001, 8193):
+        y = torch.from_numpy(rng.normal(0, 2.0, (5, vocab)).astype(np.float32)).to(torch.float16)
+        params = [SamplingParams(temperature=1.0, top_p=0.99)] * 4 + [SamplingParams(temperature=1.0)]
+        out, ref, gk, gp = run_both(fs, y, params, rng.random(5))
+        check(out, ref, params, gk, gp)
+    wide = torch.from_numpy(rng.normal(0, 3.0, (3, 151936 + 3)).astype(np.float32)).to(DEV)
+    y = wide[:, :151936]                                     # rows 151939 elements apart
+    assert y.stride(0) == 151939
+    params = [SamplingParams(temperature=1.0, top_p=0.97)] * 3
+    out, ref, _, _ = run_both(fs, y, params, np.array([0.99, 0.7, 0.95]), kept=False)
+    check(out, ref, params)
+    z = torch.from_numpy(rng.normal(0, 1.0, (2, 151936)).astype(np.float32))
+    z[:, 0] = 6.0                                             # token 0 is the maximum
+    params = [SamplingParams(temperature=1.0, top_p=0.999), SamplingParams(temperature=1.0)]
+    out, ref, gk, gp = run_both(fs, z, params, np.array([0.999, 0.999]))
+    assert (out["status"] & _lib.FIE_ROW_EXACT_PATH).all()
+    check(out, ref, params, gk, gp)
