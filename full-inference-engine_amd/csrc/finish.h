@@ -1118,10 +1118,18 @@ FIE_DEV int binned_bound(FinSmem& S, int cnt, bool use_mass, u128 g)
     __syncthreads();
     uint32_t cb = ci - cs;
     float mb = mi - ms;
-    for (int w = 0; w < wave; ++w) {
-        cb += S.red32[w];
-        mb += __uint_as_float(S.red32[kFinWaves + w]);
+    float mall = 0.0f;
+    for (int w = 0; w < kFinWaves; ++w) {
+        if (w < wave) {
+            cb += S.red32[w];
+            mb += __uint_as_float(S.red32[kFinWaves + w]);
+        }
+        mall += __uint_as_float(S.red32[kFinWaves + w]);
     }
+    // every candidate's mass together is below g, beyond the float sums' error: the
+    // crossing lies past the candidates
+    const bool beyond = use_mass &&
+        (double)mall * (1.0 + 0x1p-9) + 0x1p-26 < u128_to_double(g) * 0x1p-80 * (1.0 - 0x1p-40);
     uint32_t crun = cb;
     float mrun = mb;
 #pragma unroll
@@ -1135,6 +1143,7 @@ FIE_DEV int binned_bound(FinSmem& S, int cnt, bool use_mass, u128 g)
     __syncthreads();
     const int bc = S.ibin, bm = S.flag;
     __syncthreads();
+    if (beyond) return -2;
     return (bc < 0 || bm < 0) ? -1 : (bc > bm ? bc : bm);
 }
 
@@ -1142,6 +1151,7 @@ FIE_DEV int narrow_binned(FinSmem& S, int nv, float M, int cnt, u128 g)
 {
     const int tid = threadIdx.x;
     const int bs = binned_bound(S, cnt, true, g);
+    if (bs == -2) return -1;                     // the crossing lies past every candidate
     if (bs < 0) return nv;
     constexpr int kStage = kChunk / 2;           // S.cnt holds this many composites
     uint64_t* tmp = (uint64_t*)S.cnt;
@@ -1635,8 +1645,13 @@ FIE_DEV void finish_row(FinSmem& S, const KParams& P, const int row, const bool 
                 nv = by_mass ? narrow_binned(S, nv, M, cnt, g) : narrow_candidates(S, nv, M, cnt, false, g);
             }
 
-            sort_desc(S, nv);
-            sorted = true;
+            if (nv < 0) {
+                deep = true;                     // no need to sort what cannot settle the row
+                nv = 0;
+            } else {
+                sort_desc(S, nv);
+                sorted = true;
+            }
         }
         }
     }
