@@ -41,6 +41,8 @@ def parse():
     ap.add_argument("--config", type=int, default=3, help="headline workload C1..C5 (default C3)")
     ap.add_argument("--others", default="1,2,4,5", help="other configs to time ('' for none)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--full-row-only", action="store_true",
+                    help="time only the full-row path latencies (for a kernel trace of them)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--ring-mb", type=int, default=640)
     ap.add_argument("--lmhead-dim", type=int, default=4096,
@@ -362,6 +364,9 @@ def main() -> None:
     import torch
 
     dev = torch.device("cuda:0")
+    if a.full_row_only:
+        print(json.dumps({"full_row_path": full_row_us(dev, a.steps)}), flush=True)
+        return
     main_r = time_config(a.config, a.steps, a.warmup, a.ring_mb, dev)
     w = main_r["w"]
     B, V = main_r["B"], main_r["V"]
