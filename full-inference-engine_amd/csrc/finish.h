@@ -1904,28 +1904,34 @@ FIE_DEV bool helped_row(const KParams& P, int row)
     return k == 0 || k > kHelpTopK;
 }
 
-// Counts the workgroup in at the row; true for the last of its NS + 1 workgroups,
-// which then sees every other one's stores.  Every wave waits for its own stores to
-// complete, then one thread fences for the workgroup: a device-scope fence per wave
-// costs ~0.2 us each, serialised across the helpers.
-FIE_DEV bool arrive(FinSmem& S, const KParams& P, int row)
+// Counts the workgroup in at the row: `add` is 1, plus kArrDeep from the row's own
+// workgroup when it hands the row to the full-row path.  Returns -1, or for the
+// last of the row's NS + 1 workgroups whether the row is to be finished (0 / 1).
+// A workgroup that publishes (every helper; the row's own one only with a record
+// for the full-row path) has each wave wait for its own stores, then one thread
+// fences for the workgroup: a device-scope fence per wave costs ~0.2 us each,
+// serialised across the helpers, and one that writes back nothing the others need
+// only delays the step.  The last one acquires only when the row is to be finished.
+constexpr uint32_t kArrDeep = 1u << 16;
+
+FIE_DEV int arrive(FinSmem& S, const KParams& P, int row, uint32_t add, bool publish)
 {
-    __builtin_amdgcn_s_waitcnt(0);
+    if (publish) __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0) {
-        __threadfence();
-        const uint32_t n = atomicAdd(&P.w.harr[row], 1u);
-        const bool last = n == (uint32_t)P.NS;
+        if (publish) __threadfence();
+        const uint32_t now = atomicAdd(&P.w.harr[row], add) + add;
+        const bool last = (now & (kArrDeep - 1)) == (uint32_t)P.NS + 1;
         if (last) {
             P.w.harr[row] = 0u;              // ready for the next call
-            __threadfence();
+            if (now >> 16) __threadfence();
         }
-        S.ibin = last ? 1 : 0;
+        S.ibin = last ? (int)(now >> 16) : -1;
     }
     __syncthreads();
-    const bool last = S.ibin != 0;
+    const int r = S.ibin;
     __syncthreads();
-    return last;
+    return r;
 }
 
 // Returns true when this workgroup is to finish the row through the full-row path.
@@ -2082,7 +2088,7 @@ FIE_DEV bool span_helper(FinSmem& S, const KParams& P, const int row, const int 
             P.w.hcomp[hs * kSpan + at] = cv[k];
         }
     }
-    return arrive(S, P, row) && P.w.dfr[row].mode != 0;
+    return arrive(S, P, row, 1u, true) > 0;
 }
 
 // One workgroup per row.  A row's finish is a chain of dependent steps, so its
@@ -2106,12 +2112,9 @@ __global__ __launch_bounds__(kFinThreads, WIDE ? 2 : 4) void k_finish(const KPar
             __syncthreads();
             deep = S.dmode != 0;
             if (P.helpers && helped_row(P, blockIdx.x)) {
-                if (threadIdx.x == 0) {
-                    DeferRec d = S.dfr;
-                    if (!deep) d.mode = 0;
-                    P.w.dfr[blockIdx.x] = d;
-                }
-                deep = arrive(S, P, blockIdx.x) && deep;
+                // the record goes out only with a row for the full-row path
+                if (deep && threadIdx.x == 0) P.w.dfr[blockIdx.x] = S.dfr;
+                deep = arrive(S, P, blockIdx.x, deep ? 1u + kArrDeep : 1u, deep) > 0;
                 hd = true;
             }
         }

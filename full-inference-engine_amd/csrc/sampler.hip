@@ -601,12 +601,18 @@ int fie_sampler_sample_noalloc(const fie_sampler_args* args, void* stream)
     if (rc != FIE_OK || args->rows == 0) return rc;
     Layout L;
     if (!layout_of(args->rows, args->vocab, &L)) return fail(FIE_E_ARG, "sizes out of range");
+    int32_t ws_rows = args->rows;
+    if (L.total > FIE_SCRATCH_BYTES && ws_rows <= kHelpRows) {
+        // the span helpers' arrays do not fit: lay the array out without them
+        ws_rows = kHelpRows + 1;
+        if (!layout_of(ws_rows, args->vocab, &L)) return fail(FIE_E_ARG, "sizes out of range");
+    }
     if (L.total > FIE_SCRATCH_BYTES)
         return fail(FIE_E_WORKSPACE, "rows x vocab need more than the 64 MiB static scratch");
     void* p = nullptr;
     rc = scratch_of(&p);
     if (rc != FIE_OK) return rc;
-    const fie_workspace ws{p, FIE_SCRATCH_BYTES, args->rows, args->vocab};
+    const fie_workspace ws{p, FIE_SCRATCH_BYTES, ws_rows, args->vocab};
     return fie_sampler_sample(args, &ws, stream);
 }
 

@@ -214,7 +214,9 @@ const char* fie_sampler_last_error(void);
  * per device on the first call there and held by each device until the process
  * ends.  No counterpart in the reference: it is for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops).  Returns
- * FIE_E_WORKSPACE when fie_sampler_workspace_size(rows, vocab) exceeds the array.
+ * FIE_E_WORKSPACE when fie_sampler_workspace_size(rows, vocab) exceeds the array
+ * (for at most 16 rows: when it does even without the span helpers' arrays, which
+ * are then left out and the rows settled without helpers).
  * Calls that overlap on one device share the array and race; calls on one stream,
  * or otherwise ordered, are safe. */
 #define FIE_SCRATCH_BYTES ((size_t)64 << 20)

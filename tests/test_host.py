@@ -385,6 +385,13 @@ def test_workspace_size():
     assert lib.fie_sampler_workspace_size(1, 0) == 0
     assert lib.fie_sampler_workspace_size(1, _lib.MAX_VOCAB + 1) == 0
     assert lib.fie_sampler_workspace_size(1024, 151936) <= _lib.SCRATCH_BYTES
+    # a workspace for at most 16 rows also holds the span helpers' arrays: per row and
+    # 8192-token span, the histogram (20 KiB), the bin offsets and the span's composites
+    spans = -(-151936 // 8192)
+    helpers = 16 * spans * (1024 * 20 + 1028 * 4 + 8192 * 8)
+    assert lib.fie_sampler_workspace_size(16, 151936) >= helpers
+    assert lib.fie_sampler_workspace_size(17, 151936) < lib.fie_sampler_workspace_size(16, 151936)
+    assert lib.fie_sampler_workspace_size(16, 151936) <= _lib.SCRATCH_BYTES
 
 
 def _args(**kw):
