@@ -620,3 +620,25 @@ def test_span_helpers_lone_rows_and_odd_shapes(fs):
     out, ref, gk, gp = run_both(fs, z, params, np.array([0.999, 0.999]))
     assert (out["status"] & _lib.FIE_ROW_EXACT_PATH).all()
     check(out, ref, params, gk, gp)
+
+
+def test_span_helpers_flat_rows_repeated(fs):
+    """Twelve flat bf16 rows (top-p, min-p, a wide top-k, both, plain draws) run with
+    span helpers five times over: every call bit-exact with the oracle, whichever of
+    a row's workgroups arrives last."""
+    rng = np.random.default_rng(5)
+    x = torch.from_numpy(rng.normal(0, 0.3, (12, 151936)).astype(np.float32)).to(torch.bfloat16)
+    params = [SamplingParams(temperature=1.0, top_p=0.95), SamplingParams(temperature=1.0, min_p=0.05),
+              SamplingParams(temperature=1.0, top_k=2000),
+              SamplingParams(temperature=0.9, top_k=3000, top_p=0.97),
+              SamplingParams(temperature=1.0)] * 2 + [SamplingParams(), SamplingParams(temperature=1.0, top_p=0.5)]
+    u = rng.random(12)
+    V = x.shape[1]
+    print(f"  case: 12 flat bf16 rows x5, vocab={V}", flush=True)
+    ref = O.canonical_step(x.float().numpy(), O.resolve(params, V), u, want_kept=False)
+    hp = resolve_params(params, V, u, None)
+    xd = x.to(DEV)
+    for _ in range(5):
+        out, _, _ = fs.step(xd, hp)
+        assert (out["status"] & _lib.FIE_ROW_EXACT_PATH).sum() >= 4
+        check(out, ref, params)
